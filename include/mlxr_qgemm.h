@@ -1,0 +1,136 @@
+/*
+ * mlxr_qgemm.h -- C ABI of the MI355X (gfx950) quantized-matmul library
+ * (libmlxr_qgemm.so).
+ *
+ * It replaces the device side of MLXR's q_gemm_dequant operator:
+ *   reference  core/kernels/primitives/q_gemm_dequant_primitive.h:211-215
+ *              (mlxr::kernels::q_gemm_dequant, Y[M,N] = X[M,K] . W[N,K]^T + bias)
+ *              core/kernels/primitives/q_gemm_dequant_primitive.mm:367-450 (eval_gpu)
+ *              core/kernels/metal/q_gemm_dequant.metal:292-312,338-486 (QGemmArgs + kernel)
+ * and the weight upload the reference leaves unimplemented
+ *   reference  daemon/server/model_loader.cpp:236-245 (quantized tensors skipped)
+ *              core/runtime/mmap_loader.h:51-61 (WeightTensor host bytes)
+ *
+ * Conventions
+ *   - Every pointer named *_dev is device memory on the current HIP device; *_host is
+ *     host memory.  `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *   - All work is stream-ordered and asynchronous; no entry point synchronises the
+ *     device except mlxr_qgemm_pack (host source; it waits for its own copy).
+ *   - Return value 0 = success, negative = error (MLXR_E_*); the message of the last
+ *     error on the calling thread is returned by mlxr_qgemm_last_error().  No C++
+ *     exception crosses this boundary.
+ *   - Thread-safe: the library has no mutable global state besides the thread-local
+ *     error string.
+ *   - Dequantized weights follow the GGUF block_q8_0 / block_q4_K / block_q6_K
+ *     definitions exactly (fp32 results are bit-exact to those formulas).
+ */
+#ifndef MLXR_QGEMM_H
+#define MLXR_QGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Quantization types: same numeric values as mlxr::kernels::QuantType
+ * (reference q_gemm_dequant_primitive.h:18-35).  Implemented: Q8_0, Q4_K, Q6_K. */
+enum {
+  MLXR_Q4_0 = 0, MLXR_Q4_1 = 1, MLXR_Q8_0 = 2, MLXR_Q4_K = 3, MLXR_Q6_K = 4,
+  MLXR_Q5_0 = 5, MLXR_Q5_1 = 6, MLXR_Q8_1 = 7, MLXR_Q2_K = 8, MLXR_Q3_K = 9,
+  MLXR_Q5_K = 10, MLXR_Q8_K = 11, MLXR_IQ2_XXS = 12, MLXR_IQ2_XS = 13,
+  MLXR_IQ3_XXS = 14, MLXR_IQ3_S = 15
+};
+
+/* Element types of activations, bias and outputs. */
+enum { MLXR_F32 = 0, MLXR_F16 = 1, MLXR_BF16 = 2 };
+
+/* Status codes. */
+enum {
+  MLXR_OK = 0,
+  MLXR_E_INVALID = -1,     /* null pointer, bad dtype, non-positive size */
+  MLXR_E_UNSUPPORTED = -2, /* quant type not implemented (reference: .mm:76,133,340) */
+  MLXR_E_SHAPE = -3,       /* K not a multiple of the block size, group_size mismatch */
+  MLXR_E_HIP = -4,         /* HIP runtime error (message has the HIP error string) */
+  MLXR_E_NOMEM = -5        /* device allocation failed (mlxr_qgemm_pack only) */
+};
+
+/* Execution path selector for mlxr_qgemm_run_ex. */
+enum {
+  MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M <= 64, MFMA GEMM otherwise */
+  MLXR_PATH_GEMV = 1, /* force the wavefront-reduction GEMV kernel (any M <= 64) */
+  MLXR_PATH_MFMA = 2  /* force the bf16-MFMA GEMM (any M >= 1) */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int mlxr_qgemm_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mlxr_qgemm_last_error(void);
+
+/* Bytes of the raw GGUF tensor: N * ceil(K/group) * sizeof(block).
+ * Replaces compute_quantized_weight_size (reference .mm:116-135) and
+ * calculate_tensor_size (daemon/registry/gguf_parser.cpp:179-241, Q6_K = 210 B). */
+int mlxr_qgemm_gguf_size(int qtype, int N, int K, size_t* bytes);
+
+/* Elements per quantization group: Q8_0 -> 32, Q4_K/Q6_K -> 256
+ * (reference get_default_group_size, .mm:80-92). */
+int mlxr_qgemm_group_size(int qtype);
+
+/* Name of a quant type ("Q4_K", ...; "Unknown" otherwise) (reference .mm:94-114). */
+const char* mlxr_qgemm_type_name(int qtype);
+
+/* Bytes of the packed device buffer for an [N, K] weight of type qtype. */
+int mlxr_qgemm_packed_size(int qtype, int N, int K, size_t* bytes);
+
+/* One-time upload: repack GGUF blocks (host memory, N rows of K/group blocks, as stored
+ * in the file) into packed_dev (mlxr_qgemm_packed_size bytes).  Allocates a temporary
+ * device staging buffer, copies, repacks on the device, frees the staging buffer, and
+ * synchronises `stream` before returning. */
+int mlxr_qgemm_pack(int qtype, int N, int K, const void* gguf_host, void* packed_dev,
+                    void* stream);
+
+/* Same, from GGUF bytes already on the device.  Asynchronous, allocates nothing. */
+int mlxr_qgemm_pack_device(int qtype, int N, int K, const void* gguf_dev, void* packed_dev,
+                           void* stream);
+
+/* Dequantize a packed weight into out_dev [N, K] (row-major), out_dtype MLXR_F32
+ * (bit-exact GGUF formulas) or MLXR_BF16 (round-to-nearest-even of those fp32 values,
+ * produced by the same routine the MFMA GEMM uses to fill its LDS tiles). */
+int mlxr_qgemm_dequant(int qtype, int N, int K, const void* packed_dev, void* out_dev,
+                       int out_dtype, void* stream);
+
+/* Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]), fp32 accumulation.
+ *   x_dev    [M, K] row-major, x_dtype MLXR_BF16 or MLXR_F16
+ *   bias_dev [N] or NULL, bias_dtype MLXR_F32 / MLXR_F16 / MLXR_BF16 (ignored if NULL)
+ *   y_dev    [M, N] row-major, y_dtype MLXR_F32 / MLXR_F16 / MLXR_BF16
+ *   group_size must be 0 (use the type's default) or equal to mlxr_qgemm_group_size.
+ * Arguments mirror q_gemm_dequant(input, weights, M, N, K, quant_type, group_size, bias)
+ * (reference q_gemm_dequant_primitive.h:211-215) with the weights already packed. */
+int mlxr_qgemm_run(int qtype, int N, int K, int group_size, const void* packed_dev,
+                   const void* x_dev, int x_dtype, const void* bias_dev, int bias_dtype,
+                   void* y_dev, int y_dtype, int M, void* stream);
+
+/* mlxr_qgemm_run with an explicit path (MLXR_PATH_*). */
+int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packed_dev,
+                      const void* x_dev, int x_dtype, const void* bias_dev, int bias_dtype,
+                      void* y_dev, int y_dtype, int M, int path, void* stream);
+
+/* Deterministic synthetic inputs with the shapes/distributions of the benchmark
+ * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by
+ * Box-Muller in double precision.
+ *   Q8_0: d = RNE_fp16(|N(0,1)| * 0.02/127), qs uniform in [-127, 127]
+ *   Q4_K: d, dmin = RNE_fp16(|N(0,1)| * 1e-3), 12 scale bytes and 128 qs bytes uniform
+ *   Q6_K: ql, qh bytes uniform, scales uniform in [-32, 31], d = RNE_fp16(|N(0,1)|*1e-3)
+ * out_host must hold mlxr_qgemm_gguf_size bytes. */
+int mlxr_synth_gguf(int qtype, int N, int K, uint64_t seed, void* out_host);
+
+/* count values of N(0,1) rounded (RNE) to dtype MLXR_BF16 / MLXR_F16 / MLXR_F32. */
+int mlxr_synth_act(size_t count, int dtype, uint64_t seed, void* out_host);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLXR_QGEMM_H */

@@ -1,0 +1,176 @@
+// extern "C" boundary of libmlxr_qgemm.so (declared in include/mlxr_qgemm.h).
+//
+// Validation and error behaviour follow the reference operator
+// (core/kernels/primitives/q_gemm_dequant_primitive.mm:478-522 shape checks,
+// :76/:133/:340 unsupported types) but as status codes plus a thread-local message:
+// no exception crosses the C ABI.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/mlxr_qgemm.h"
+#include "qgemm_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  return fail(MLXR_E_HIP, "%s: HIP error %d (%s)", where, (int)e, hipGetErrorString(e));
+}
+
+bool implemented(int qtype) {
+  return qtype == MLXR_Q8_0 || qtype == MLXR_Q4_K || qtype == MLXR_Q6_K;
+}
+
+int check_type_shape(int qtype, int N, int K, mlxr::PackedLayout* L) {
+  if (qtype < 0 || qtype > MLXR_IQ3_S) return fail(MLXR_E_INVALID, "invalid quant type %d", qtype);
+  if (!implemented(qtype))
+    return fail(MLXR_E_UNSUPPORTED, "Unsupported quantization type %s", mlxr_qgemm_type_name(qtype));
+  if (N <= 0 || K <= 0) return fail(MLXR_E_INVALID, "N and K must be positive (N=%d, K=%d)", N, K);
+  const int g = mlxr::gguf_block_elems(qtype);
+  if (K % g != 0)
+    return fail(MLXR_E_SHAPE, "K=%d is not a multiple of the %s block size %d", K,
+                mlxr_qgemm_type_name(qtype), g);
+  if (!mlxr::make_layout(qtype, N, K, L)) return fail(MLXR_E_SHAPE, "cannot lay out %dx%d", N, K);
+  return MLXR_OK;
+}
+
+bool valid_dtype(int dt) { return dt == MLXR_F32 || dt == MLXR_F16 || dt == MLXR_BF16; }
+
+}  // namespace
+
+extern "C" {
+
+int mlxr_qgemm_version(void) { return 10000; }
+
+const char* mlxr_qgemm_last_error(void) { return g_err.c_str(); }
+
+const char* mlxr_qgemm_type_name(int qtype) {
+  static const char* names[] = {"Q4_0", "Q4_1", "Q8_0",    "Q4_K",   "Q6_K",    "Q5_0",
+                                "Q5_1", "Q8_1", "Q2_K",    "Q3_K",   "Q5_K",    "Q8_K",
+                                "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S"};
+  if (qtype < 0 || qtype > 15) return "Unknown";
+  return names[qtype];
+}
+
+int mlxr_qgemm_group_size(int qtype) {
+  // reference get_default_group_size (.mm:80-92): 256 for the K-quants, 32 otherwise
+  // (types beyond Q6_K fall back to 32 there as well).
+  return (qtype == MLXR_Q4_K || qtype == MLXR_Q6_K) ? 256 : 32;
+}
+
+int mlxr_qgemm_gguf_size(int qtype, int N, int K, size_t* bytes) {
+  if (!bytes) return fail(MLXR_E_INVALID, "bytes is null");
+  if (N <= 0 || K <= 0) return fail(MLXR_E_INVALID, "N and K must be positive (N=%d, K=%d)", N, K);
+  const int g = mlxr::gguf_block_elems(qtype), bb = mlxr::gguf_block_bytes(qtype);
+  if (g == 0) return fail(MLXR_E_UNSUPPORTED, "Unsupported quantization type %s", mlxr_qgemm_type_name(qtype));
+  *bytes = (size_t)N * (size_t)((K + g - 1) / g) * (size_t)bb;
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_packed_size(int qtype, int N, int K, size_t* bytes) {
+  if (!bytes) return fail(MLXR_E_INVALID, "bytes is null");
+  mlxr::PackedLayout L;
+  const int rc = check_type_shape(qtype, N, K, &L);
+  if (rc) return rc;
+  *bytes = L.total;
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_pack_device(int qtype, int N, int K, const void* gguf_dev, void* packed_dev,
+                           void* stream) {
+  mlxr::PackedLayout L;
+  const int rc = check_type_shape(qtype, N, K, &L);
+  if (rc) return rc;
+  if (!gguf_dev || !packed_dev) return fail(MLXR_E_INVALID, "null buffer");
+  const hipError_t e = mlxr::launch_pack(L, (const uint8_t*)gguf_dev, (uint8_t*)packed_dev, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "pack launch");
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_pack(int qtype, int N, int K, const void* gguf_host, void* packed_dev, void* stream) {
+  mlxr::PackedLayout L;
+  int rc = check_type_shape(qtype, N, K, &L);
+  if (rc) return rc;
+  if (!gguf_host || !packed_dev) return fail(MLXR_E_INVALID, "null buffer");
+  size_t bytes = 0;
+  mlxr_qgemm_gguf_size(qtype, N, K, &bytes);
+  hipStream_t s = (hipStream_t)stream;
+  void* staging = nullptr;
+  hipError_t e = hipMalloc(&staging, bytes);
+  if (e != hipSuccess) return fail(MLXR_E_NOMEM, "staging allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+  e = hipMemcpyAsync(staging, gguf_host, bytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = mlxr::launch_pack(L, (const uint8_t*)staging, (uint8_t*)packed_dev, s);
+  const hipError_t es = hipStreamSynchronize(s);
+  (void)hipFree(staging);
+  if (e != hipSuccess) return hip_fail(e, "pack");
+  if (es != hipSuccess) return hip_fail(es, "pack sync");
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_dequant(int qtype, int N, int K, const void* packed_dev, void* out_dev, int out_dtype,
+                       void* stream) {
+  mlxr::PackedLayout L;
+  const int rc = check_type_shape(qtype, N, K, &L);
+  if (rc) return rc;
+  if (!packed_dev || !out_dev) return fail(MLXR_E_INVALID, "null buffer");
+  if (out_dtype != MLXR_F32 && out_dtype != MLXR_BF16)
+    return fail(MLXR_E_INVALID, "dequant output dtype must be F32 or BF16 (got %d)", out_dtype);
+  const hipError_t e = mlxr::launch_dequant(L, (const uint8_t*)packed_dev, out_dev, out_dtype, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "dequant launch");
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packed_dev, const void* x_dev,
+                      int x_dtype, const void* bias_dev, int bias_dtype, void* y_dev, int y_dtype, int M,
+                      int path, void* stream) {
+  mlxr::RunArgs a;
+  int rc = check_type_shape(qtype, N, K, &a.L);
+  if (rc) return rc;
+  if (group_size != 0 && group_size != mlxr_qgemm_group_size(qtype))
+    return fail(MLXR_E_SHAPE, "group_size %d does not match %s (block of %d)", group_size,
+                mlxr_qgemm_type_name(qtype), mlxr_qgemm_group_size(qtype));
+  if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
+  if (x_dtype != MLXR_BF16 && x_dtype != MLXR_F16)
+    return fail(MLXR_E_INVALID, "activation dtype must be BF16 or F16 (got %d)", x_dtype);
+  if (!valid_dtype(y_dtype)) return fail(MLXR_E_INVALID, "invalid output dtype %d", y_dtype);
+  if (bias_dev && !valid_dtype(bias_dtype)) return fail(MLXR_E_INVALID, "invalid bias dtype %d", bias_dtype);
+  if (path < MLXR_PATH_AUTO || path > MLXR_PATH_MFMA) return fail(MLXR_E_INVALID, "invalid path %d", path);
+  if (M == 0) return MLXR_OK;
+  if (!packed_dev || !x_dev || !y_dev) return fail(MLXR_E_INVALID, "null buffer");
+  if (path == MLXR_PATH_GEMV && M > 64)
+    return fail(MLXR_E_INVALID, "the GEMV path takes M <= 64 (M=%d)", M);
+  a.packed = (const uint8_t*)packed_dev;
+  a.x = x_dev;
+  a.x_dtype = x_dtype;
+  a.bias = bias_dev;
+  a.bias_dtype = bias_dtype;
+  a.y = y_dev;
+  a.y_dtype = y_dtype;
+  a.M = M;
+  const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= 64);
+  const hipError_t e = gemv ? mlxr::launch_gemv(a, (hipStream_t)stream) : mlxr::launch_mfma(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, gemv ? "gemv launch" : "mfma launch");
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_run(int qtype, int N, int K, int group_size, const void* packed_dev, const void* x_dev,
+                   int x_dtype, const void* bias_dev, int bias_dtype, void* y_dev, int y_dtype, int M,
+                   void* stream) {
+  return mlxr_qgemm_run_ex(qtype, N, K, group_size, packed_dev, x_dev, x_dtype, bias_dev, bias_dtype, y_dev,
+                           y_dtype, M, MLXR_PATH_AUTO, stream);
+}
+
+}  // extern "C"

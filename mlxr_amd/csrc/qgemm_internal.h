@@ -1,0 +1,43 @@
+// Internal launcher interface between the C ABI (qgemm_api.hip) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "qgemm_layout.h"
+
+namespace mlxr {
+
+struct PlanePtrs {
+  const uint8_t* p[4];
+};
+
+inline PlanePtrs plane_ptrs(const PackedLayout& L, const uint8_t* base) {
+  PlanePtrs P;
+  for (int i = 0; i < 4; ++i) P.p[i] = (i < L.nplanes) ? base + L.off[i] : nullptr;
+  return P;
+}
+
+// Arguments of one Y = X . W^T (+ bias) call, validated by the caller.
+struct RunArgs {
+  PackedLayout L;
+  const uint8_t* packed;
+  const void* x;
+  int x_dtype;
+  const void* bias;  // may be null
+  int bias_dtype;
+  void* y;
+  int y_dtype;
+  int M;
+};
+
+hipError_t launch_pack(const PackedLayout& L, const uint8_t* gguf_dev, uint8_t* packed_dev,
+                       hipStream_t s);
+hipError_t launch_dequant(const PackedLayout& L, const uint8_t* packed_dev, void* out,
+                          int out_dtype, hipStream_t s);
+
+// Wavefront-reduction GEMV / skinny GEMM, no MFMA.  Requires 1 <= M <= 64.
+hipError_t launch_gemv(const RunArgs& a, hipStream_t s);
+
+// LDS-dequant bf16 MFMA GEMM.  Any M >= 1 (rows beyond M are masked).
+hipError_t launch_mfma(const RunArgs& a, hipStream_t s);
+
+}  // namespace mlxr

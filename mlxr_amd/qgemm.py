@@ -1,0 +1,229 @@
+"""Python host side of the quantized matmul: ctypes over libmlxr_qgemm.so.
+
+Mirrors the reference operator (core/kernels/primitives/q_gemm_dequant_primitive.h):
+``QuantType`` keeps the enum values (:18-35), ``q_gemm_dequant(input, weights, M, N, K,
+quant_type, group_size, bias)`` keeps the argument order and meaning (:211-215), and
+errors raise ``RuntimeError`` subclasses with the messages of the reference where it has
+one (.mm:490-496).  torch tensors are used only as device memory and streams; every
+computation runs in the HIP library, and the module raises if that library is missing.
+"""
+import ctypes
+import enum
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libmlxr_qgemm.so")
+
+F32, F16, BF16 = 0, 1, 2
+PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+
+
+class QuantType(enum.IntEnum):
+    Q4_0 = 0
+    Q4_1 = 1
+    Q8_0 = 2
+    Q4_K = 3
+    Q6_K = 4
+    Q5_0 = 5
+    Q5_1 = 6
+    Q8_1 = 7
+    Q2_K = 8
+    Q3_K = 9
+    Q5_K = 10
+    Q8_K = 11
+    IQ2_XXS = 12
+    IQ2_XS = 13
+    IQ3_XXS = 14
+    IQ3_S = 15
+
+
+class QGemmError(RuntimeError):
+    """A nonzero status from the C ABI; ``code`` holds the MLXR_E_* value."""
+
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+_lib = None
+
+_SIGS = {
+    "mlxr_qgemm_version": (ctypes.c_int, []),
+    "mlxr_qgemm_last_error": (ctypes.c_char_p, []),
+    "mlxr_qgemm_gguf_size": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]),
+    "mlxr_qgemm_group_size": (ctypes.c_int, [ctypes.c_int]),
+    "mlxr_qgemm_type_name": (ctypes.c_char_p, [ctypes.c_int]),
+    "mlxr_qgemm_packed_size": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]),
+    "mlxr_qgemm_pack": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "mlxr_qgemm_pack_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "mlxr_qgemm_dequant": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
+    "mlxr_qgemm_run": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "mlxr_qgemm_run_ex": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
+    "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
+}
+
+
+def lib():
+    """The loaded HIP library.  Raises if it has not been built (no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m mlxr_amd.build` "
+                               "(there is no non-HIP implementation)")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise QGemmError(rc, lib().mlxr_qgemm_last_error().decode())
+
+
+# ----------------------------------------------------------------- metadata helpers
+
+def gguf_size(qtype, N, K):
+    """N * ceil(K/group) * sizeof(block) (reference compute_quantized_weight_size)."""
+    v = ctypes.c_size_t()
+    _check(lib().mlxr_qgemm_gguf_size(int(qtype), N, K, ctypes.byref(v)))
+    return v.value
+
+
+compute_quantized_weight_size = gguf_size
+
+
+def packed_size(qtype, N, K):
+    v = ctypes.c_size_t()
+    _check(lib().mlxr_qgemm_packed_size(int(qtype), N, K, ctypes.byref(v)))
+    return v.value
+
+
+def get_default_group_size(qtype):
+    return lib().mlxr_qgemm_group_size(int(qtype))
+
+
+def quant_type_name(qtype):
+    return lib().mlxr_qgemm_type_name(int(qtype)).decode()
+
+
+_BPW = {QuantType.Q4_0: 18 / 32, QuantType.Q4_1: 20 / 32, QuantType.Q8_0: 34 / 32,
+        QuantType.Q4_K: 144 / 256, QuantType.Q6_K: 210 / 256}
+
+
+def get_bytes_per_weight(qtype):
+    """Bytes per weight (reference QGemmDequantPrimitive::get_bytes_per_weight, .mm:63-78)."""
+    try:
+        return _BPW[QuantType(qtype)]
+    except (KeyError, ValueError):
+        raise QGemmError(-2, "Unsupported quantization type") from None
+
+
+# ------------------------------------------------------------------ synthetic inputs
+
+def synth_gguf(qtype, N, K, seed):
+    """Deterministic GGUF blocks (numpy uint8) with the benchmark distributions."""
+    out = np.empty(gguf_size(qtype, N, K), dtype=np.uint8)
+    _check(lib().mlxr_synth_gguf(int(qtype), N, K, seed, out.ctypes.data))
+    return out
+
+
+def synth_act(count, dtype, seed):
+    """count N(0,1) values rounded to dtype (BF16/F16 -> uint16 bits, F32 -> float32)."""
+    out = np.empty(count, dtype=np.float32 if dtype == F32 else np.uint16)
+    _check(lib().mlxr_synth_act(count, dtype, seed, out.ctypes.data))
+    return out
+
+
+# ------------------------------------------------------------------ device operations
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream_ptr(stream):
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _dt_code(dtype):
+    torch = _torch()
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[dtype]
+
+
+class PackedWeight:
+    """A weight repacked into the library's HBM layout (device uint8 tensor)."""
+
+    def __init__(self, buf, qtype, N, K):
+        self.buf, self.qtype, self.N, self.K = buf, QuantType(qtype), N, K
+
+    def data_ptr(self):
+        return self.buf.data_ptr()
+
+    @property
+    def nbytes(self):
+        return self.buf.numel()
+
+
+def pack_weights(gguf, N, K, qtype, device="cuda", stream=None):
+    """One-time upload of GGUF blocks (numpy/CPU tensor/device tensor) to the packed layout."""
+    torch = _torch()
+    buf = torch.empty(packed_size(qtype, N, K), dtype=torch.uint8, device=device)
+    need = gguf_size(qtype, N, K)
+    if isinstance(gguf, np.ndarray):
+        gguf = torch.from_numpy(np.ascontiguousarray(gguf).view(np.uint8).reshape(-1))
+    if gguf.numel() * gguf.element_size() < need:
+        raise QGemmError(-1, "weights buffer is smaller than N * K/group * sizeof(block)")
+    if gguf.device.type == "cpu":
+        gguf = gguf.to(device, non_blocking=False)
+    _check(lib().mlxr_qgemm_pack_device(int(qtype), N, K, gguf.data_ptr(), buf.data_ptr(), _stream_ptr(stream)))
+    if stream is None:
+        torch.cuda.current_stream().synchronize()  # the staging tensor may be freed after return
+    return PackedWeight(buf, qtype, N, K)
+
+
+def dequantize(pw, dtype=None, stream=None):
+    """[N, K] fp32 (bit-exact GGUF formulas) or bf16 (RNE of those) from a packed weight."""
+    torch = _torch()
+    dtype = dtype or torch.float32
+    out = torch.empty((pw.N, pw.K), dtype=dtype, device=pw.buf.device)
+    _check(lib().mlxr_qgemm_dequant(int(pw.qtype), pw.N, pw.K, pw.data_ptr(), out.data_ptr(),
+                                    _dt_code(dtype), _stream_ptr(stream)))
+    return out
+
+
+def q_gemm_dequant(input, weights, M, N, K, quant_type, group_size=0, bias=None, out=None,
+                   out_dtype=None, path=PATH_AUTO, stream=None):
+    """Y[M,N] = input[M,K] . W[N,K]^T (+ bias), fp32 accumulation.
+
+    Same arguments as the reference's q_gemm_dequant (q_gemm_dequant_primitive.h:211-215).
+    ``weights`` is a PackedWeight, or raw GGUF bytes (uint8 tensor on the device) which are
+    packed for this call.  Output dtype defaults to the input dtype.
+    """
+    torch = _torch()
+    if input.dim() != 2 or input.shape[0] != M or input.shape[1] != K:
+        raise QGemmError(-3, "Input shape must be [M, K]")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != N):
+        raise QGemmError(-3, "Bias shape must be [N]")
+    if not isinstance(weights, PackedWeight):
+        weights = pack_weights(weights, N, K, quant_type, device=input.device, stream=stream)
+    elif (weights.qtype, weights.N, weights.K) != (QuantType(quant_type), N, K):
+        raise QGemmError(-3, "packed weights do not match (quant_type, N, K)")
+    if not input.is_contiguous():
+        input = input.contiguous()
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or input.dtype, device=input.device)
+    _check(lib().mlxr_qgemm_run_ex(int(quant_type), N, K, group_size, weights.data_ptr(), input.data_ptr(),
+                                   _dt_code(input.dtype), bias.data_ptr() if bias is not None else None,
+                                   _dt_code(bias.dtype) if bias is not None else F32, out.data_ptr(),
+                                   _dt_code(out.dtype), M, path, _stream_ptr(stream)))
+    return out

@@ -1,0 +1,156 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle.
+
+Bars: packed bytes and fp32 dequant bit-exact; bf16 dequant bit-exact to RNE_bf16 of the
+oracle; matmul outputs within max|y-ref|/max|ref| <= 5e-3 of the fp64-accumulated oracle
+(GEMV over the exact weights, MFMA over the bf16-rounded weights it consumes).
+"""
+import numpy as np
+import pytest
+
+import mlxr_amd as mx
+from oracle import orc
+from tests import packref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-3
+Q4K, Q6K, Q80 = mx.QuantType.Q4_K, mx.QuantType.Q6_K, mx.QuantType.Q8_0
+
+
+def _dev_bytes(torch, arr, device):
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(device)
+
+
+def _act(torch, M, K, dtype_code, seed, device):
+    bits = mx.synth_act(M * K, dtype_code, seed)
+    t = torch.from_numpy(bits.view(np.int16).reshape(M, K)).to(device)
+    t = t.view(torch.bfloat16 if dtype_code == mx.BF16 else torch.float16)
+    xf = (orc.bf16_bits_to_f32(bits) if dtype_code == mx.BF16 else orc.f16_bits_to_f32(bits)).reshape(M, K)
+    return t, xf
+
+
+def _packed(torch, qt, N, K, seed, device):
+    w = mx.synth_gguf(qt, N, K, seed)
+    return w, mx.pack_weights(w, N, K, qt, device=device)
+
+
+@pytest.mark.parametrize("qt,N,K", [(Q4K, 64, 1024), (Q6K, 48, 768), (Q80, 40, 2048), (Q4K, 3, 256)])
+def test_pack_bytes_match_layout(cuda, qt, N, K):
+    import torch
+    w = mx.synth_gguf(qt, N, K, 11)
+    pw = mx.pack_weights(w, N, K, qt, device=cuda)
+    got = pw.buf.cpu().numpy()
+    ref_planes = packref.planes(int(qt), N, K, w)
+    off = 0
+    for p in ref_planes:
+        np.testing.assert_array_equal(got[off:off + p.size], p)
+        off = (off + p.size + 255) & ~255
+    assert off == pw.nbytes
+
+
+@pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 256, 2048), (Q4K, 1, 256)])
+def test_dequant_f32_bit_exact(cuda, qt, N, K):
+    import torch
+    w, pw = _packed(torch, qt, N, K, 21, cuda)
+    got = mx.dequantize(pw, torch.float32).cpu().numpy()
+    ref = orc.dequant(int(qt), N, K, w)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 64, 2048)])
+def test_dequant_bf16_rne_bit_exact(cuda, qt, N, K):
+    import torch
+    w, pw = _packed(torch, qt, N, K, 22, cuda)
+    got = mx.dequantize(pw, torch.bfloat16).cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = orc.dequant(int(qt), N, K, w)
+    refb = torch.from_numpy(ref).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, refb)
+
+
+GEMV_CASES = [
+    (Q4K, 1, 512, 1024), (Q4K, 1, 1000, 2304), (Q4K, 3, 257, 4096), (Q4K, 8, 128, 512),
+    (Q4K, 16, 96, 768), (Q4K, 33, 64, 1024), (Q4K, 64, 80, 512),
+    (Q6K, 1, 300, 2048), (Q6K, 5, 128, 1280), (Q6K, 64, 64, 512),
+    (Q80, 1, 256, 2048), (Q80, 2, 100, 96), (Q80, 40, 64, 1024),
+]
+
+
+@pytest.mark.parametrize("xdt", [mx.BF16, mx.F16])
+@pytest.mark.parametrize("qt,M,N,K", GEMV_CASES)
+def test_gemv_matches_oracle(cuda, qt, M, N, K, xdt):
+    import torch
+    w, pw = _packed(torch, qt, N, K, 31 + M, cuda)
+    x, xf = _act(torch, M, K, xdt, 41 + N, cuda)
+    y = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_GEMV)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf)
+    err = orc.normwise_rel_err(y.cpu().numpy(), ref)
+    assert err <= TOL, err
+    # the GEMV accumulates exact products in fp32: far tighter than the contract
+    assert err <= 1e-5, err
+
+
+MFMA_CASES = [
+    (Q4K, 128, 256, 1024), (Q4K, 130, 200, 512), (Q4K, 1, 128, 256), (Q4K, 256, 384, 2048),
+    (Q6K, 128, 128, 1024), (Q6K, 200, 96, 512), (Q80, 128, 160, 1024), (Q80, 77, 64, 96),
+]
+
+
+@pytest.mark.parametrize("qt,M,N,K", MFMA_CASES)
+def test_mfma_matches_oracle(cuda, qt, M, N, K):
+    import torch
+    w, pw = _packed(torch, qt, N, K, 51 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 61 + N, cuda)
+    y = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
+    err = orc.normwise_rel_err(y.cpu().numpy(), ref)
+    assert err <= TOL, err
+    # against the exact (unrounded) weights the bf16 rounding still stays in contract
+    ref_exact = orc.gemm_f64(int(qt), M, N, K, w, xf)
+    assert orc.normwise_rel_err(y.cpu().numpy(), ref_exact) <= TOL
+
+
+def test_mfma_f16_activations(cuda):
+    import torch
+    qt, M, N, K = Q4K, 160, 192, 1024
+    w, pw = _packed(torch, qt, N, K, 71, cuda)
+    x, xf = _act(torch, M, K, mx.F16, 72, cuda)
+    y = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    assert orc.normwise_rel_err(y.cpu().numpy(), orc.gemm_f64(int(qt), M, N, K, w, xf)) <= TOL
+
+
+@pytest.mark.parametrize("path", [mx.PATH_GEMV, mx.PATH_MFMA])
+@pytest.mark.parametrize("ydt", ["bf16", "f16", "f32"])
+def test_bias_and_output_dtypes(cuda, path, ydt):
+    import torch
+    qt, M, N, K = Q4K, 4 if path == mx.PATH_GEMV else 136, 200, 512
+    w, pw = _packed(torch, qt, N, K, 81, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 82, cuda)
+    bias_f = np.linspace(-1, 1, N).astype(np.float32)
+    bias = torch.from_numpy(bias_f).to(cuda).to(torch.bfloat16)
+    bias_ref = bias.float().cpu().numpy()
+    odt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[ydt]
+    y = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=odt, path=path)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bias_ref, w_to_bf16=(path == mx.PATH_MFMA))
+    assert y.dtype == odt
+    assert orc.normwise_rel_err(y.float().cpu().numpy(), ref) <= TOL
+
+
+def test_raw_gguf_weights_are_packed_per_call(cuda):
+    import torch
+    qt, M, N, K = Q6K, 2, 64, 512
+    w = mx.synth_gguf(qt, N, K, 91)
+    x, xf = _act(torch, M, K, mx.BF16, 92, cuda)
+    y = mx.q_gemm_dequant(x, torch.from_numpy(w).to(cuda), M, N, K, qt, out_dtype=torch.float32)
+    assert orc.normwise_rel_err(y.cpu().numpy(), orc.gemm_f64(int(qt), M, N, K, w, xf)) <= TOL
+
+
+def test_gemv_rows_independent_of_batch(cuda):
+    """M-tiling invariance: row m of an M=64 call equals the M=1 call on row m, bit for bit."""
+    import torch
+    qt, N, K = Q4K, 512, 4096
+    w, pw = _packed(torch, qt, N, K, 101, cuda)
+    x, _ = _act(torch, 64, K, mx.BF16, 102, cuda)
+    y64 = mx.q_gemm_dequant(x, pw, 64, N, K, qt, out_dtype=torch.float32, path=mx.PATH_GEMV)
+    for m in (0, 17, 63):
+        y1 = mx.q_gemm_dequant(x[m:m + 1], pw, 1, N, K, qt, out_dtype=torch.float32, path=mx.PATH_GEMV)
+        assert torch.equal(y1[0], y64[m])
