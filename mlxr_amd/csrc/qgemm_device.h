@@ -49,13 +49,14 @@ __host__ __device__ constexpr int q6h_shift(int e) {
   return 2 * ((e & 7) >> 1) + 16 * (e & 1) + 8 * ((e >> 3) & 1);
 }
 
-// Q4_K: scale (bits 0..5) and min (bits 6..11) of sub-block j from the 12-byte field
-// area held in three little-endian words h1..h3 of the 16-byte header.
-__device__ __forceinline__ uint32_t q4k_field(uint32_t h1, uint32_t h2, uint32_t h3, int j) {
-  const uint64_t lo = ((uint64_t)h2 << 32) | h1;
-  const uint64_t hi = ((uint64_t)h3 << 32) | h2;
-  const uint64_t v = (j < 4) ? (lo >> (12 * j)) : (hi >> (12 * j - 32));
-  return (uint32_t)v & 0xfffu;
+// Q4_K lane-sliced header (8 x u16 per super-block): d | dmin << 16 from the high
+// nibbles of all eight entries.
+__device__ __forceinline__ uint32_t q4k_dd(const uint4& h) {
+  const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+  uint32_t dd = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dd |= ((w[j >> 1] >> (16 * (j & 1) + 12)) & 15u) << (4 * j);
+  return dd;
 }
 
 // Dequantize sub-block `sb` (32 weights along K) of row n to fp32, exactly as the GGUF
@@ -68,9 +69,11 @@ __device__ __forceinline__ void dequant_sub_f32(const uint8_t* const* planes, in
     const size_t nsb = (size_t)(K / 256);
     const uint4 q = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
     const uint4 h = *(const uint4*)(planes[1] + ((size_t)n * nsb + (sb >> 3)) * 16);
-    const uint32_t f = q4k_field(h.y, h.z, h.w, sb & 7);
-    const float dsc = f16_bits_to_f32(h.x & 0xffffu) * (float)(f & 63u);
-    const float dm = f16_bits_to_f32(h.x >> 16) * (float)(f >> 6);
+    const uint32_t dd = q4k_dd(h);
+    const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+    const uint32_t f = (hw[(sb & 7) >> 1] >> (16 * (sb & 1))) & 0xfffu;
+    const float dsc = f16_bits_to_f32(dd & 0xffffu) * (float)(f & 63u);
+    const float dm = f16_bits_to_f32(dd >> 16) * (float)(f >> 6);
     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int e = 0; e < 32; ++e) {

@@ -16,6 +16,8 @@
 // Work split: one workgroup = 4 wavefronts; a wavefront owns R output rows and walks K
 // in segments of 64 sub-blocks (2048 weights), lane i taking sub-block 64*seg + i.  The
 // lane's 32 activations are loaded once per segment and reused for all R rows.
+#include <stdlib.h>
+
 #include "qgemm_device.h"
 #include "qgemm_internal.h"
 
@@ -24,6 +26,9 @@ namespace mlxr {
 namespace {
 
 enum XType : int { X_BF16 = 0, X_F16 = 1 };
+
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
 
 struct GemvParams {
   PlanePtrs P;
@@ -85,6 +90,19 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (a + b) + (c + d);
 }
 
+// Sum over the 64 lanes: DPP adds within rows of 16 (quad swaps, half-row and row
+// mirrors), then row_bcast:15 / row_bcast:31 carry the row totals upward so lane 63 holds
+// the wavefront total; returned as a uniform value.
+__device__ __forceinline__ float wave_total(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *(const uint4*)p; }
 
 // Weights of one row and one sub-block, as loaded from HBM.
@@ -92,7 +110,8 @@ template <int QT>
 struct WLoad;
 template <>
 struct WLoad<QT_Q4_K> {
-  uint4 q, h;
+  uint4 q;
+  uint32_t h;  // this lane's u16 of the lane-sliced header
 };
 template <>
 struct WLoad<QT_Q6_K> {
@@ -107,23 +126,34 @@ struct WLoad<QT_Q8_0> {
   uint32_t d;
 };
 
-template <int QT>
+template <bool NT>
+__device__ __forceinline__ uint4 ldw16(const uint8_t* p) {
+  typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+  if constexpr (NT) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+  } else {
+    return *(const uint4*)p;
+  }
+}
+
+template <int QT, bool NT = false>
 __device__ __forceinline__ void load_w(const PlanePtrs& P, int K, int n, int sb, WLoad<QT>& w) {
   const size_t nsub = (size_t)(K >> 5);
   if constexpr (QT == QT_Q4_K) {
     const size_t nsb = (size_t)(K >> 8);
-    w.q = ld16(P.p[0] + ((size_t)n * nsub + sb) * 16);
-    w.h = ld16(P.p[1] + ((size_t)n * nsb + (sb >> 3)) * 16);
+    w.q = ldw16<NT>(P.p[0] + ((size_t)n * nsub + sb) * 16);
+    w.h = *(const uint16_t*)(P.p[1] + ((size_t)n * nsb + (sb >> 3)) * 16 + 2 * (sb & 7));
   } else if constexpr (QT == QT_Q6_K) {
     const size_t nsb = (size_t)(K >> 8);
-    w.ql = ld16(P.p[0] + ((size_t)n * nsub + sb) * 16);
+    w.ql = ldw16<NT>(P.p[0] + ((size_t)n * nsub + sb) * 16);
     w.qh = *(const uint2*)(P.p[1] + ((size_t)n * nsub + sb) * 8);
     w.sc = *(const uint16_t*)(P.p[2] + ((size_t)n * nsb + (sb >> 3)) * 16 + 2 * (sb & 7));
     w.d = *(const uint16_t*)(P.p[3] + ((size_t)n * nsb + (sb >> 3)) * 2);
   } else {
     const uint8_t* q = P.p[0] + ((size_t)n * nsub + sb) * 32;
-    w.a = ld16(q);
-    w.b = ld16(q + 16);
+    w.a = ldw16<NT>(q);
+    w.b = ldw16<NT>(q + 16);
     w.d = *(const uint16_t*)(P.p[1] + ((size_t)n * nsub + sb) * 2);
   }
 }
@@ -131,7 +161,7 @@ template <int QT>
 __device__ __forceinline__ void zero_w(WLoad<QT>& w) {
   if constexpr (QT == QT_Q4_K) {
     w.q = make_uint4(0, 0, 0, 0);
-    w.h = make_uint4(0, 0, 0, 0);
+    w.h = 0;
   } else if constexpr (QT == QT_Q6_K) {
     w.ql = make_uint4(0, 0, 0, 0);
     w.qh = make_uint2(0, 0);
@@ -159,9 +189,14 @@ __device__ __forceinline__ void decode_w(const WLoad<QT>& w, int j, WDec& o) {
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int s = 0; s < 4; ++s) o.p[4 * t + s] = ((qw[t] >> (4 * s)) & 0x000F000Fu) | MAGIC;
-    const uint32_t f = q4k_field(w.h.y, w.h.z, w.h.w, j);
-    o.s0 = f16_bits_to_f32(w.h.x & 0xffffu) * (float)(f & 63u);
-    o.s1 = f16_bits_to_f32(w.h.x >> 16) * (float)(f >> 6);
+    // d | dmin << 16: nibble j of it sits in bits 12..15 of lane j's entry; OR the eight
+    // lanes of the super-block together (xor 1, xor 2 within quads, then mirror within 8).
+    uint32_t dd = (w.h >> 12) << (4 * j);
+    dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0xB1, 0xF, 0xF, false);
+    dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0x4E, 0xF, 0xF, false);
+    dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0x141, 0xF, 0xF, false);
+    o.s0 = f16_bits_to_f32(dd & 0xffffu) * (float)(w.h & 63u);
+    o.s1 = f16_bits_to_f32(dd >> 16) * (float)((w.h >> 6) & 63u);
   } else if constexpr (QT == QT_Q6_K) {
     constexpr uint32_t MAGIC = (XT == X_BF16) ? 0x43004300u : 0x64006400u;
     const uint32_t lw[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
@@ -304,6 +339,333 @@ __global__ __launch_bounds__(256) void qgemv_kernel(GemvParams p) {
   }
 }
 
+// Variant for M <= 4 (the decode shapes).  Each wavefront owns a contiguous run of rows
+// and walks them as a flat sequence of (row, segment) chunks, D-1 chunks of loads in
+// flight ahead of the one being reduced.  Weight loads are raw buffer loads whose row /
+// segment offset is a scalar (SGPR) and whose lane offset is fixed, so a chunk costs no
+// vector address arithmetic; lanes past the end of K get an offset beyond the buffer and
+// read zeros.  The activations (and their per-sub-block sums) are staged once per
+// workgroup in LDS as [m][segment][quarter][lane] so each chunk reads them with
+// conflict-free 16-byte LDS loads at immediate offsets.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t OOB = 0x80000000u;  // voffset that is out of range of every buffer
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* ptr, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int QT>
+struct CLoad;
+// 16-bit fields stay 16-bit until decoded: widening them in the loop latch would make
+// the compiler wait for the loads in flight.
+template <>
+struct CLoad<QT_Q4_K> {
+  uint4 q;
+  uint16_t h;
+};
+template <>
+struct CLoad<QT_Q6_K> {
+  uint4 ql;
+  uint2 qh;
+  uint16_t sc, d;
+};
+template <>
+struct CLoad<QT_Q8_0> {
+  uint4 a, b;
+  uint16_t d;
+};
+
+// (v & mask) | bits in one VALU op; the compiler otherwise emits an and plus an or.
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(bits));
+  return r;
+}
+
+struct LdsParams {
+  GemvParams g;
+  uint32_t psize[4];  // plane sizes in bytes (all < 2^31)
+  uint32_t cmask, cmagic;  // 0x000F000F and the bf16/fp16 magic, passed at run time
+  int rows_per_wave;
+};
+
+template <int QT>
+__device__ __forceinline__ void load_chunk(const rsrc_t* R, int row, int seg, int nsub, int nsb,
+                                           int lane, bool ok, CLoad<QT>& b) {
+  const uint32_t sbase = (uint32_t)row * (uint32_t)nsub + (uint32_t)seg * 64u;  // first sub-block
+  const uint32_t gbase = (uint32_t)row * (uint32_t)nsb + (uint32_t)seg * 8u;    // first super-block
+  if constexpr (QT == QT_Q4_K) {
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    b.q = make_uint4(q[0], q[1], q[2], q[3]);
+    b.h = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, gbase * 16u, 0);
+  } else if constexpr (QT == QT_Q6_K) {
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    b.ql = make_uint4(q[0], q[1], q[2], q[3]);
+    const u32x2_t h = __builtin_amdgcn_raw_buffer_load_b64(R[1], ok ? lane * 8 : OOB, sbase * 8u, 0);
+    b.qh = make_uint2(h[0], h[1]);
+    b.sc = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, 0);
+    b.d = __builtin_amdgcn_raw_buffer_load_b16(R[3], ok ? (lane >> 3) * 2 : OOB, gbase * 2u, 0);
+  } else {
+    const u32x4_t q0 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 : OOB, sbase * 32u, 0);
+    const u32x4_t q1 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 + 16 : OOB, sbase * 32u, 0);
+    b.a = make_uint4(q0[0], q0[1], q0[2], q0[3]);
+    b.b = make_uint4(q1[0], q1[1], q1[2], q1[3]);
+    b.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, sbase * 2u, 0);
+  }
+}
+
+template <int QT, int XT>
+__device__ __forceinline__ void decode_chunk(const CLoad<QT>& b, int j, uint32_t MASK, uint32_t MAGIC, WDec& o) {
+  if constexpr (QT == QT_Q4_K) {
+    const uint32_t qw[4] = {b.q.x, b.q.y, b.q.z, b.q.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) o.p[4 * t + s] = and_or(qw[t] >> (4 * s), MASK, MAGIC);
+    // d | dmin << 16: nibble j of it sits in bits 12..15 of lane j's entry; OR the eight
+    // lanes of the super-block together (xor 1, xor 2 within quads, then mirror within 8).
+    const uint32_t hv = b.h;
+    uint32_t dd = (hv >> 12) << (4 * j);
+    dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0xB1, 0xF, 0xF, false);
+    dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0x4E, 0xF, 0xF, false);
+    dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0x141, 0xF, 0xF, false);
+    o.s0 = f16_bits_to_f32(dd & 0xffffu) * (float)(hv & 63u);
+    o.s1 = f16_bits_to_f32(dd >> 16) * (float)((hv >> 6) & 63u);
+  } else if constexpr (QT == QT_Q6_K) {
+    WLoad<QT_Q6_K> w;
+    w.ql = b.ql;
+    w.qh = b.qh;
+    w.sc = b.sc;
+    w.d = b.d;
+    decode_w<QT, XT>(w, j, o);
+  } else {
+    WLoad<QT_Q8_0> w;
+    w.a = b.a;
+    w.b = b.b;
+    w.d = b.d;
+    decode_w<QT, XT>(w, j, o);
+  }
+}
+
+template <int QT, int XT, int MT, int D, bool LIN>
+__global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const GemvParams& p = lp.g;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps the loop scalar
+  const int K = p.K, N = p.N, M = p.M;
+  const int nsub = K >> 5, nsb = K >> 8;
+  const int nseg = (nsub + 63) >> 6;
+  const int rpw = lp.rows_per_wave;
+  const int r0 = (blockIdx.x * 4 + wave) * rpw;
+  const int r1 = min(r0 + rpw, N);
+  const int C = r1 > r0 ? (r1 - r0) * nseg : 0;
+  uint4* xs = (uint4*)smem;                                          // [MT][nseg][4][64]
+  float2* Xs = (float2*)(smem + (size_t)MT * nseg * 4096);           // [MT][nseg][64]
+
+  rsrc_t R[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, lp.psize[i]);
+
+  // Activation loads go out first (two padded tasks per thread; padding reads zeros),
+  // then the weight prefetch, so the in-order memory counter never makes the LDS staging
+  // wait for HBM.
+  const rsrc_t RX = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+  const int T = MT * nseg * 64;
+  auto xoff = [&](int t) -> uint32_t {
+    const int m = t / (nseg * 64), sbp = t - m * nseg * 64;
+    return (t < T && m < M && sbp < nsub) ? ((uint32_t)m * K + (uint32_t)sbp * 32u) * 2u : OOB;
+  };
+  auto xload = [&](int t, uint4* v) {
+    const uint32_t o = xoff(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(RX, o + 16 * i, 0, 0);
+      v[i] = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  };
+  uint4 xa[4], xc[4];
+  xload(threadIdx.x, xa);
+  if (T > 256) xload(threadIdx.x + 256, xc);
+
+  CLoad<QT> buf[D];
+  auto issue = [&](int c, CLoad<QT>& b) {
+    const int cc = max(min(c, C - 1), 0);
+    if constexpr (LIN) {
+      // every row is exactly nseg full segments: chunk cc starts at sub-block r0*nsub + 64*cc
+      load_chunk<QT>(R, r0, cc, nsub, nsb, lane, true, b);
+    } else {
+      const int rl = cc / nseg, seg = cc - rl * nseg;
+      const int row = min(r0 + rl, N - 1);
+      load_chunk<QT>(R, row, seg, nsub, nsb, lane, seg * 64 + lane < nsub, b);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) issue(d, buf[d]);
+
+  auto stage = [&](int t, const uint4* v) {
+    const int m = t / (nseg * 64), sbp = t - m * nseg * 64;
+    const int seg = sbp >> 6, l = sbp & 63;
+    uint32_t xv[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xs[((m * nseg + seg) * 4 + i) * 64 + l] = v[i];
+      xv[4 * i + 0] = v[i].x;
+      xv[4 * i + 1] = v[i].y;
+      xv[4 * i + 2] = v[i].z;
+      xv[4 * i + 3] = v[i].w;
+    }
+    float2 X;
+    X.x = sum_range<XT, 0, 8>(xv);
+    X.y = sum_range<XT, 8, 16>(xv);
+    Xs[(m * nseg + seg) * 64 + l] = X;
+  };
+  if ((int)threadIdx.x < T) stage(threadIdx.x, xa);
+  if ((int)threadIdx.x + 256 < T) stage(threadIdx.x + 256, xc);
+  for (int t = threadIdx.x + 512; t < T; t += 256) {
+    uint4 v[4];
+    xload(t, v);
+    stage(t, v);
+  }
+  __syncthreads();
+  if (C == 0) return;
+
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+  float res = 0.f;
+  const uint32_t MASK = lp.cmask, MAGIC = lp.cmagic;
+
+  auto compute = [&](const CLoad<QT>& b, const int rl, const int seg) {
+    WDec wd;
+    decode_chunk<QT, XT>(b, lane & 7, MASK, MAGIC, wd);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < M) {
+        const uint4* xp = xs + (m * nseg + seg) * 256 + lane;
+        uint32_t xv[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint4 v = xp[64 * i];
+          xv[4 * i + 0] = v.x;
+          xv[4 * i + 1] = v.y;
+          xv[4 * i + 2] = v.z;
+          xv[4 * i + 3] = v.w;
+        }
+        const float2 X = Xs[(m * nseg + seg) * 64 + lane];
+        acc[m] += contrib<QT, XT>(xv, wd, X.x, X.y);
+      }
+    }
+    if (seg == nseg - 1) {
+      // Row finished: its total goes to lane (row_local * MT + m); stored after the loop.
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m < M) {
+          const float tot = wave_total(acc[m]);
+          res = (lane == rl * MT + m) ? tot : res;
+        }
+        acc[m] = 0.f;
+      }
+    }
+  };
+
+  // Steady state: D chunks per trip, every load and compute unconditional.
+  // (row_local, segment) of the chunk being reduced: uniform loop state.
+  int c = 0, rl = 0, seg = 0;
+  for (; c + D <= C; c += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      issue(c + d + D - 1, buf[(d + D - 1) % D]);
+      compute(buf[d], rl, seg);
+      if (++seg == nseg) {
+        seg = 0;
+        ++rl;
+      }
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    if (c + d < C) {
+      compute(buf[d], rl, seg);
+      if (++seg == nseg) {
+        seg = 0;
+        ++rl;
+      }
+    }
+  }
+
+  // Lane (row_local * MT + m) holds y[m, r0 + row_local].
+  const int orl = lane / MT, om = lane - orl * MT;
+  if (orl < r1 - r0 && om < M) {
+    float v = res;
+    if (p.bias) v += load_scalar(p.bias, p.bias_dtype, (size_t)(r0 + orl));
+    store_scalar(p.y, p.y_dtype, (size_t)om * N + r0 + orl, v);
+  }
+}
+
+size_t lds_bytes(int MT, int K) { return (size_t)MT * (size_t)(((K >> 5) + 63) >> 6) * 64 * 72; }
+
+int num_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cus = v;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+int waves_per_cu_target() {
+  static int w = 0;
+  if (w == 0) {
+    const char* e = getenv("MLXR_GEMV_WAVES_PER_CU");
+    w = e ? atoi(e) : 16;
+    if (w <= 0) w = 16;
+  }
+  return w;
+}
+
+int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
+
+template <int QT, int XT, int MT, int D>
+hipError_t launch_lds_t(const LdsParams& lp, unsigned grid, hipStream_t s) {
+  if (((lp.g.K >> 5) & 63) == 0)
+    qgemv_lds_kernel<QT, XT, MT, D, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.g.K), s>>>(lp);
+  else
+    qgemv_lds_kernel<QT, XT, MT, D, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.g.K), s>>>(lp);
+  return hipGetLastError();
+}
+
+// Planes addressed with 32-bit buffer offsets: every plane (and x) must stay below 2 GiB.
+bool lds_fits(const GemvParams& p, const PackedLayout& L, int MT) {
+  for (int i = 0; i < L.nplanes; ++i)
+    if (L.size[i] >= (1u << 31)) return false;
+  if ((size_t)p.M * p.K * 2 >= (1u << 31)) return false;
+  return lds_bytes(MT, p.K) <= 65536;
+}
+
+template <int QT, int XT, int MT>
+hipError_t launch_lds(const GemvParams& p, const PackedLayout& L, hipStream_t s) {
+  static const int depth = env_int("MLXR_GEMV_DEPTH", 3);
+  LdsParams lp;
+  lp.g = p;
+  for (int i = 0; i < 4; ++i) lp.psize[i] = i < L.nplanes ? (uint32_t)L.size[i] : 0u;
+  lp.cmask = 0x000F000Fu;
+  lp.cmagic = XT == X_BF16 ? 0x43004300u : 0x64006400u;
+  const int target = num_cus() * waves_per_cu_target();
+  lp.rows_per_wave = min((p.N + target - 1) / target, 64 / MT);  // row results are held one per lane
+  const int waves = (p.N + lp.rows_per_wave - 1) / lp.rows_per_wave;
+  const unsigned grid = (unsigned)((waves + 3) / 4);
+  if (depth >= 4) return launch_lds_t<QT, XT, MT, 4>(lp, grid, s);
+  return launch_lds_t<QT, XT, MT, 3>(lp, grid, s);
+}
+
 template <int QT, int XT, int MT, int R>
 hipError_t launch_t(const GemvParams& p, hipStream_t s) {
   const int rows_per_block = 4 * R;
@@ -313,8 +675,13 @@ hipError_t launch_t(const GemvParams& p, hipStream_t s) {
 }
 
 template <int QT, int XT>
-hipError_t launch_x(const GemvParams& p, int R, hipStream_t s) {
+hipError_t launch_x(const GemvParams& p, const PackedLayout& L, int R, hipStream_t s) {
   const int M = p.M;
+  if (M <= 4 && lds_fits(p, L, M == 1 ? 1 : M <= 2 ? 2 : 4)) {
+    if (M == 1) return launch_lds<QT, XT, 1>(p, L, s);
+    if (M == 2) return launch_lds<QT, XT, 2>(p, L, s);
+    return launch_lds<QT, XT, 4>(p, L, s);
+  }
   if (M == 1) {
     if (R >= 4) return launch_t<QT, XT, 1, 4>(p, s);
     if (R == 2) return launch_t<QT, XT, 1, 2>(p, s);
@@ -351,9 +718,9 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s) {
   const int R = pick_rows(p.N);
   const bool f16 = a.x_dtype == DT_F16;
   switch (a.L.qtype) {
-    case QT_Q4_K: return f16 ? launch_x<QT_Q4_K, X_F16>(p, R, s) : launch_x<QT_Q4_K, X_BF16>(p, R, s);
-    case QT_Q6_K: return f16 ? launch_x<QT_Q6_K, X_F16>(p, R, s) : launch_x<QT_Q6_K, X_BF16>(p, R, s);
-    default: return f16 ? launch_x<QT_Q8_0, X_F16>(p, R, s) : launch_x<QT_Q8_0, X_BF16>(p, R, s);
+    case QT_Q4_K: return f16 ? launch_x<QT_Q4_K, X_F16>(p, a.L, R, s) : launch_x<QT_Q4_K, X_BF16>(p, a.L, R, s);
+    case QT_Q6_K: return f16 ? launch_x<QT_Q6_K, X_F16>(p, a.L, R, s) : launch_x<QT_Q6_K, X_BF16>(p, a.L, R, s);
+    default: return f16 ? launch_x<QT_Q8_0, X_F16>(p, a.L, R, s) : launch_x<QT_Q8_0, X_BF16>(p, a.L, R, s);
   }
 }
 

@@ -14,8 +14,10 @@
 // (word >> 4s) & 0x000F000F puts weight 2s in bits 0..3 and weight 2s+1 in bits 16..19.
 //
 //   Q4_K  plane 0  qs   [N][nsub][16 B]  sub-block = 4 pair-interleaved words (q 0..15)
-//         plane 1  hdr  [N][K/256][16 B] fp16 d | fp16 dmin | 12 B holding eight 12-bit
-//                                        fields f_j = sc_j | m_j << 6 at bit 12j (LE)
+//         plane 1  hdr  [N][K/256][8 x u16] lane-sliced header: u16 j (one per sub-block)
+//                                        = sc_j | m_j << 6 | nibble j of (d | dmin << 16) << 12,
+//                                        so the lane that owns sub-block j loads 2 bytes and
+//                                        rebuilds d, dmin with an OR across the 8 lanes
 //   Q6_K  plane 0  ql   [N][nsub][16 B]  low 4 bits, 4 pair-interleaved words
 //         plane 1  qh   [N][nsub][8 B]   high 2 bits; for word t (weights 8t..8t+7) of
 //                                        the sub-block: u32 index t/2, weight 8t+2s at

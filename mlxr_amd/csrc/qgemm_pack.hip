@@ -24,8 +24,9 @@ __global__ void pack_q4k_kernel(const uint8_t* __restrict__ src, uint8_t* __rest
   const uint8_t* b = src + idx * 144;
   const uint8_t* s = b + 4;
   const uint8_t* q = b + 16;
-  // header: d | dmin | eight 12-bit (sc | m << 6) fields
-  uint32_t f[3] = {0u, 0u, 0u};
+  // header: u16 j = sc_j | m_j << 6 | (nibble j of d | dmin << 16) << 12
+  const uint32_t dd = rd_u16(b, 0) | (rd_u16(b, 2) << 16);
+  uint16_t* h = (uint16_t*)(hdr_out + idx * 16);
   for (int j = 0; j < 8; ++j) {
     uint32_t sc, m;
     if (j < 4) {
@@ -35,17 +36,8 @@ __global__ void pack_q4k_kernel(const uint8_t* __restrict__ src, uint8_t* __rest
       sc = (s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
       m = (uint32_t)(s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
     }
-    const uint32_t v = sc | (m << 6);
-    for (int bit = 0; bit < 12; ++bit) {
-      const int pos = 12 * j + bit;
-      f[pos >> 5] |= ((v >> bit) & 1u) << (pos & 31);
-    }
+    h[j] = (uint16_t)(sc | (m << 6) | (((dd >> (4 * j)) & 15u) << 12));
   }
-  uint32_t* h = (uint32_t*)(hdr_out + idx * 16);
-  h[0] = rd_u16(b, 0) | (rd_u16(b, 2) << 16);
-  h[1] = f[0];
-  h[2] = f[1];
-  h[3] = f[2];
   // qs: sub-block j = 64-chunk j/2, low (j even) or high (j odd) nibbles
   uint32_t* o = (uint32_t*)(qs_out + idx * 128);
   for (int j = 0; j < 8; ++j) {

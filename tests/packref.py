@@ -48,13 +48,12 @@ def planes(qtype, N, K, gguf):
         nsb = K // 256
         b = g.reshape(N, nsb, 144)
         sc, m = q4k_scale_min(b[..., 4:16])
-        f = (sc | (m << 6)).astype(np.uint64)
-        bits = np.zeros((N, nsb, 96), np.uint8)
+        dd = (b[..., 0].astype(np.uint32) | (b[..., 1].astype(np.uint32) << 8)
+              | (b[..., 2].astype(np.uint32) << 16) | (b[..., 3].astype(np.uint32) << 24))
+        hdr = np.zeros((N, nsb, 8), np.uint16)
         for j in range(8):
-            for bit in range(12):
-                bits[..., 12 * j + bit] = ((f[..., j] >> np.uint64(bit)) & np.uint64(1)).astype(np.uint8)
-        fbytes = np.packbits(bits, axis=-1, bitorder="little")
-        hdr = np.concatenate([b[..., 0:4], fbytes], axis=-1)  # [N, nsb, 16]
+            hdr[..., j] = (sc[..., j] | (m[..., j] << 6) | (((dd >> np.uint32(4 * j)) & 15) << 12)).astype(np.uint16)
+        hdr = hdr.view(np.uint8).reshape(N, nsb, 16)
         qs = b[..., 16:144].reshape(N, nsb, 4, 32)
         nib = np.stack([qs & 15, qs >> 4], axis=3).reshape(N, nsb, 8, 32)  # sub-block 2c, 2c+1
         words = _words_from_nibbles(nib)  # [N, nsb, 8, 4]

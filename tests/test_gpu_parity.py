@@ -145,12 +145,18 @@ def test_raw_gguf_weights_are_packed_per_call(cuda):
 
 
 def test_gemv_rows_independent_of_batch(cuda):
-    """M-tiling invariance: row m of an M=64 call equals the M=1 call on row m, bit for bit."""
+    """M-tiling invariance.  Within one kernel variant (M <= 4 share the LDS-staged kernel)
+    row m of a batched call equals the M=1 call on row m bit for bit; the M=64 call runs the
+    register-staged variant, whose reduction order differs, so it must agree to fp32
+    rounding."""
     import torch
     qt, N, K = Q4K, 512, 4096
     w, pw = _packed(torch, qt, N, K, 101, cuda)
     x, _ = _act(torch, 64, K, mx.BF16, 102, cuda)
+    y3 = mx.q_gemm_dequant(x[:3].contiguous(), pw, 3, N, K, qt, out_dtype=torch.float32, path=mx.PATH_GEMV)
     y64 = mx.q_gemm_dequant(x, pw, 64, N, K, qt, out_dtype=torch.float32, path=mx.PATH_GEMV)
-    for m in (0, 17, 63):
+    for m in (0, 1, 2, 17, 63):
         y1 = mx.q_gemm_dequant(x[m:m + 1], pw, 1, N, K, qt, out_dtype=torch.float32, path=mx.PATH_GEMV)
-        assert torch.equal(y1[0], y64[m])
+        if m < 3:
+            assert torch.equal(y1[0], y3[m])
+        assert orc.normwise_rel_err(y1[0].cpu().numpy(), y64[m].cpu().numpy()) <= 1e-6
