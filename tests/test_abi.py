@@ -1,0 +1,127 @@
+"""C-ABI library checks that need no GPU: it loads, exports every symbol the headers
+declare, reports sizes/names like the reference helpers, and rejects bad arguments with
+the documented status codes before touching a device."""
+import ctypes
+import os
+import re
+import subprocess
+import threading
+
+import numpy as np
+import pytest
+
+import mlxr_amd as mx
+from mlxr_amd import qgemm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HDR = os.path.join(ROOT, "include", "mlxr_qgemm.h")
+
+
+def test_exports_every_declared_symbol():
+    names = set(re.findall(r"\b(mlxr_\w+)\s*\(", open(HDR).read()))
+    assert len(names) >= 13
+    lib = ctypes.CDLL(qgemm.LIB_PATH)
+    for n in sorted(names):
+        assert hasattr(lib, n), n
+    # the C++ operator interface is exported too
+    out = subprocess.run(["nm", "-D", "--defined-only", qgemm.LIB_PATH], capture_output=True, text=True).stdout
+    for sym in ("q_gemm_dequant", "pack_weights", "compute_quantized_weight_size", "quant_type_name",
+                "QGemmDequantPrimitive"):
+        assert sym in out
+
+
+def test_metadata_matches_reference_helpers():
+    assert mx.lib().mlxr_qgemm_version() >= 10000
+    assert [mx.quant_type_name(t) for t in range(16)] == [
+        "Q4_0", "Q4_1", "Q8_0", "Q4_K", "Q6_K", "Q5_0", "Q5_1", "Q8_1", "Q2_K", "Q3_K", "Q5_K", "Q8_K",
+        "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S"]
+    assert mx.quant_type_name(99) == "Unknown"
+    assert mx.get_default_group_size(mx.QuantType.Q8_0) == 32
+    assert mx.get_default_group_size(mx.QuantType.Q4_K) == 256
+    assert mx.get_default_group_size(mx.QuantType.Q6_K) == 256
+    assert mx.gguf_size(mx.QuantType.Q4_K, 14336, 4096) == 33030144
+    assert mx.gguf_size(mx.QuantType.Q6_K, 8192, 28672) == 192675840
+    assert mx.gguf_size(mx.QuantType.Q8_0, 2048, 2048) == 4456448
+    assert mx.gguf_size(mx.QuantType.Q4_0, 1, 32) == 18  # reference parser test: Q4_0 = 18 B / 32
+    assert mx.get_bytes_per_weight(mx.QuantType.Q4_K) < 1.0
+    for qt, N, K in ((3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048), (3, 3, 256)):
+        ps, gs = mx.packed_size(qt, N, K), mx.gguf_size(qt, N, K)
+        assert gs <= ps < gs + 4 * 256  # same bytes, planes 256-byte aligned
+
+
+def _err(fn):
+    with pytest.raises(mx.QGemmError) as e:
+        fn()
+    return e.value
+
+
+def test_error_paths():
+    L = mx.lib()
+    e = _err(lambda: mx.packed_size(mx.QuantType.Q4_0, 16, 256))
+    assert e.code == -2 and "Unsupported quantization type Q4_0" in str(e)
+    e = _err(lambda: mx.packed_size(mx.QuantType.Q4_K, 16, 300))
+    assert e.code == -3 and "multiple" in str(e)
+    e = _err(lambda: mx.packed_size(mx.QuantType.Q6_K, 0, 256))
+    assert e.code == -1
+    run = L.mlxr_qgemm_run_ex
+    p = ctypes.c_void_p(8)
+    assert run(3, 16, 256, 128, p, p, 2, None, 0, p, 2, 1, 0, None) == -3  # group size mismatch
+    assert run(3, 16, 256, 0, p, p, 0, None, 0, p, 2, 1, 0, None) == -1    # fp32 activations
+    assert run(3, 16, 256, 0, p, p, 2, None, 0, p, 7, 1, 0, None) == -1    # bad output dtype
+    assert run(3, 16, 256, 0, p, p, 2, p, 9, p, 2, 1, 0, None) == -1       # bad bias dtype
+    assert run(3, 16, 256, 0, p, p, 2, None, 0, p, 2, 65, 1, None) == -1   # GEMV path, M > 64
+    assert run(3, 16, 256, 0, p, p, 2, None, 0, p, 2, 1, 5, None) == -1    # bad path
+    assert run(3, 16, 256, 0, None, p, 2, None, 0, p, 2, 1, 0, None) == -1  # null weights
+    assert run(3, 16, 256, 0, p, p, 2, None, 0, p, 2, -1, 0, None) == -1   # negative M
+    assert run(3, 16, 256, 0, p, p, 2, None, 0, p, 2, 0, 0, None) == 0     # M = 0: nothing to do
+    assert L.mlxr_qgemm_dequant(3, 16, 256, p, p, 1, None) == -1          # fp16 dequant output
+    assert L.mlxr_qgemm_pack_device(3, 16, 256, None, p, None) == -1
+
+
+def test_last_error_is_thread_local():
+    L = mx.lib()
+    assert L.mlxr_qgemm_packed_size(0, 1, 32, ctypes.byref(ctypes.c_size_t())) == -2
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(L.mlxr_qgemm_last_error()))
+    t.start()
+    t.join()
+    assert seen == [b""]
+    assert b"Q4_0" in L.mlxr_qgemm_last_error()
+
+
+def test_python_operator_shape_checks():
+    torch = pytest.importorskip("torch")
+    x = torch.zeros((2, 256), dtype=torch.bfloat16)
+    w = torch.zeros(mx.gguf_size(3, 8, 256), dtype=torch.uint8)
+    with pytest.raises(mx.QGemmError, match=r"Input shape must be \[M, K\]"):
+        mx.q_gemm_dequant(x, w, 1, 8, 256, mx.QuantType.Q4_K, 256)
+    with pytest.raises(mx.QGemmError, match=r"Bias shape must be \[N\]"):
+        mx.q_gemm_dequant(x, w, 2, 8, 256, mx.QuantType.Q4_K, 256, bias=torch.zeros(9))
+
+
+def test_synthetic_generators():
+    a = mx.synth_gguf(mx.QuantType.Q6_K, 64, 512, 5)
+    assert np.array_equal(a, mx.synth_gguf(mx.QuantType.Q6_K, 64, 512, 5))
+    assert not np.array_equal(a, mx.synth_gguf(mx.QuantType.Q6_K, 64, 512, 6))
+    b6 = a.reshape(-1, 210)
+    sc = b6[:, 192:208].view(np.int8)
+    assert sc.min() == -32 and sc.max() == 31
+    d6 = b6[:, 208:210].copy().view(np.float16).astype(np.float64)
+    assert (d6 >= 0).all() and 0.6e-3 < d6.mean() < 1.0e-3  # E|N(0,1)| * 1e-3 = 0.798e-3
+    q8 = mx.synth_gguf(mx.QuantType.Q8_0, 256, 1024, 7).reshape(-1, 34)
+    qs = q8[:, 2:].view(np.int8)
+    assert qs.min() == -127 and qs.max() == 127
+    d8 = q8[:, 0:2].copy().view(np.float16).astype(np.float64)
+    assert 0.6 * 0.02 / 127 < d8.mean() < 1.0 * 0.02 / 127
+    x = mx.synth_act(100000, mx.F32, 9)
+    assert abs(x.mean()) < 0.02 and abs(x.std() - 1) < 0.02
+
+
+def test_cpp_operator_interface(tmp_path):
+    exe = tmp_path / "test_q_gemm_api"
+    cmd = ["g++", "-std=c++17", "-O1", "-I", os.path.join(ROOT, "include"),
+           os.path.join(ROOT, "tests", "cpp", "test_q_gemm_api.cpp"), "-o", str(exe),
+           "-L", os.path.dirname(qgemm.LIB_PATH), "-lmlxr_qgemm", "-Wl,-rpath," + os.path.dirname(qgemm.LIB_PATH)]
+    subprocess.run(cmd, check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.startswith("OK"), r.stdout + r.stderr
