@@ -26,8 +26,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+// Two floats -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ float load_scalar(const void* p, int dtype, size_t i) {
@@ -59,54 +62,154 @@ __device__ __forceinline__ uint32_t q4k_dd(const uint4& h) {
   return dd;
 }
 
-// Dequantize sub-block `sb` (32 weights along K) of row n to fp32, exactly as the GGUF
-// formulas define (every product below is exact in fp32; Q4_K rounds once in the fma).
+// Raw packed bytes of one 32-weight sub-block (what a loader prefetches).
 template <int QT>
-__device__ __forceinline__ void dequant_sub_f32(const uint8_t* const* planes, int K, int n,
-                                                int sb, float* w) {
+struct RawSub;
+template <>
+struct RawSub<QT_Q4_K> {
+  uint4 q;  // 4 pair-interleaved words
+  uint4 h;  // the super-block's 8 x u16 lane-sliced header
+};
+template <>
+struct RawSub<QT_Q6_K> {
+  uint4 ql;
+  uint2 qh;
+  uint32_t sc;  // two int8 scales (groups 2j, 2j+1) in the low 16 bits
+  uint32_t d;   // fp16 bits
+};
+template <>
+struct RawSub<QT_Q8_0> {
+  uint4 a, b;
+  uint32_t d;
+};
+
+template <int QT>
+__device__ __forceinline__ void load_raw_sub(const uint8_t* const* planes, int K, int n, int sb, RawSub<QT>& r) {
   const size_t nsub = (size_t)(K / 32);
   if constexpr (QT == QT_Q4_K) {
     const size_t nsb = (size_t)(K / 256);
-    const uint4 q = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
-    const uint4 h = *(const uint4*)(planes[1] + ((size_t)n * nsb + (sb >> 3)) * 16);
-    const uint32_t dd = q4k_dd(h);
-    const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
-    const uint32_t f = (hw[(sb & 7) >> 1] >> (16 * (sb & 1))) & 0xfffu;
+    r.q = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
+    r.h = *(const uint4*)(planes[1] + ((size_t)n * nsb + (sb >> 3)) * 16);
+  } else if constexpr (QT == QT_Q6_K) {
+    const size_t nsb = (size_t)(K / 256);
+    r.ql = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
+    r.qh = *(const uint2*)(planes[1] + ((size_t)n * nsub + sb) * 8);
+    r.sc = *(const uint16_t*)(planes[2] + ((size_t)n * nsb + (sb >> 3)) * 16 + 2 * (sb & 7));
+    r.d = *(const uint16_t*)(planes[3] + ((size_t)n * nsb + (sb >> 3)) * 2);
+  } else {  // Q8_0: block index == sub-block index
+    const uint8_t* qs = planes[0] + ((size_t)n * nsub + sb) * 32;
+    r.a = *(const uint4*)qs;
+    r.b = *(const uint4*)(qs + 16);
+    r.d = *(const uint16_t*)(planes[1] + ((size_t)n * nsub + sb) * 2);
+  }
+}
+
+template <int QT>
+__device__ __forceinline__ void zero_raw_sub(RawSub<QT>& r) {
+  if constexpr (QT == QT_Q4_K) {
+    r.q = make_uint4(0, 0, 0, 0);
+    r.h = make_uint4(0, 0, 0, 0);
+  } else if constexpr (QT == QT_Q6_K) {
+    r.ql = make_uint4(0, 0, 0, 0);
+    r.qh = make_uint2(0, 0);
+    r.sc = 0;
+    r.d = 0;
+  } else {
+    r.a = make_uint4(0, 0, 0, 0);
+    r.b = make_uint4(0, 0, 0, 0);
+    r.d = 0;
+  }
+}
+
+// fp32 weights of one sub-block, exactly as the GGUF formulas define (every product
+// below is exact in fp32; Q4_K rounds once, in the fma).  j = sub-block index within its
+// super-block (sb % 8).
+template <int QT>
+__device__ __forceinline__ void dequant_raw(const RawSub<QT>& r, int j, float* w) {
+  if constexpr (QT == QT_Q4_K) {
+    const uint32_t dd = q4k_dd(r.h);
+    const uint32_t hw[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+    const uint32_t f = (hw[j >> 1] >> (16 * (j & 1))) & 0xfffu;
     const float dsc = f16_bits_to_f32(dd & 0xffffu) * (float)(f & 63u);
     const float dm = f16_bits_to_f32(dd >> 16) * (float)(f >> 6);
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
       const uint32_t v = (qw[e >> 3] >> pi_shift(e & 7)) & 15u;
       w[e] = __builtin_fmaf(dsc, (float)v, -dm);
     }
   } else if constexpr (QT == QT_Q6_K) {
-    const size_t nsb = (size_t)(K / 256);
-    const uint4 ql = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
-    const uint2 qh = *(const uint2*)(planes[1] + ((size_t)n * nsub + sb) * 8);
-    const int8_t* sc = (const int8_t*)(planes[2] + ((size_t)n * nsb + (sb >> 3)) * 16) + 2 * (sb & 7);
-    const float d = f16_bits_to_f32(*(const uint16_t*)(planes[3] + ((size_t)n * nsb + (sb >> 3)) * 2));
-    const float ds0 = d * (float)sc[0], ds1 = d * (float)sc[1];
-    const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w};
-    const uint32_t hw[2] = {qh.x, qh.y};
+    const float d = f16_bits_to_f32(r.d);
+    const float ds0 = d * (float)(int8_t)(r.sc & 0xffu), ds1 = d * (float)(int8_t)((r.sc >> 8) & 0xffu);
+    const uint32_t lw[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
+    const uint32_t hw[2] = {r.qh.x, r.qh.y};
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
       const uint32_t lo = (lw[e >> 3] >> pi_shift(e & 7)) & 15u;
       const uint32_t hi = (hw[e >> 4] >> q6h_shift(e)) & 3u;
       w[e] = (e < 16 ? ds0 : ds1) * (float)((int)(lo | (hi << 4)) - 32);
     }
-  } else {  // Q8_0: block index == sub-block index
-    const int8_t* qs = (const int8_t*)(planes[0] + ((size_t)n * nsub + sb) * 32);
-    const float d = f16_bits_to_f32(*(const uint16_t*)(planes[1] + ((size_t)n * nsub + sb) * 2));
-    const uint4 a = *(const uint4*)qs;
-    const uint4 b = *(const uint4*)(qs + 16);
-    const uint32_t qw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  } else {
+    const float d = f16_bits_to_f32(r.d);
+    const uint32_t qw[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
       const int v = (int)(int8_t)((qw[e >> 2] >> (8 * (e & 3))) & 0xffu);
       w[e] = (float)v * d;
     }
   }
+}
+
+// The same weights rounded to bf16 (RNE) and packed in K order: out[c] holds weights
+// 8c..8c+7.  `nib` must be 0x0F0F0F0F; it is passed at run time so the compiler keeps the
+// byte-select converts (v_cvt_f32_ubyte0..3) instead of folding them into bit-field
+// extracts.  Every fp32 value is the same single-rounded fma as dequant_raw.
+template <int QT>
+__device__ __forceinline__ void dequant_raw_bf16(const RawSub<QT>& r, int j, uint32_t nib, uint4* out) {
+  if constexpr (QT == QT_Q4_K) {
+    const uint32_t dd = q4k_dd(r.h);
+    const uint32_t hw[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+    const uint32_t f = (hw[j >> 1] >> (16 * (j & 1))) & 0xfffu;
+    const float dsc = f16_bits_to_f32(dd & 0xffffu) * (float)(f & 63u);
+    const float ndm = -(f16_bits_to_f32(dd >> 16) * (float)(f >> 6));
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    uint32_t o[16];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      // pair-interleaved word: bytes of (w & nib) are weights 0, 4, 1, 5 of the word,
+      // bytes of ((w >> 4) & nib) are weights 2, 6, 3, 7
+      const uint32_t lo = qw[t] & nib, hi = (qw[t] >> 4) & nib;
+      const float e0 = __builtin_fmaf(dsc, (float)(lo & 0xffu), ndm);
+      const float e4 = __builtin_fmaf(dsc, (float)((lo >> 8) & 0xffu), ndm);
+      const float e1 = __builtin_fmaf(dsc, (float)((lo >> 16) & 0xffu), ndm);
+      const float e5 = __builtin_fmaf(dsc, (float)(lo >> 24), ndm);
+      const float e2 = __builtin_fmaf(dsc, (float)(hi & 0xffu), ndm);
+      const float e6 = __builtin_fmaf(dsc, (float)((hi >> 8) & 0xffu), ndm);
+      const float e3 = __builtin_fmaf(dsc, (float)((hi >> 16) & 0xffu), ndm);
+      const float e7 = __builtin_fmaf(dsc, (float)(hi >> 24), ndm);
+      o[4 * t + 0] = pack_bf16x2(e0, e1);
+      o[4 * t + 1] = pack_bf16x2(e2, e3);
+      o[4 * t + 2] = pack_bf16x2(e4, e5);
+      o[4 * t + 3] = pack_bf16x2(e6, e7);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) out[c] = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+  } else {
+    float w[32];
+    dequant_raw<QT>(r, j, w);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      out[c] = make_uint4(pack_bf16x2(w[8 * c + 0], w[8 * c + 1]), pack_bf16x2(w[8 * c + 2], w[8 * c + 3]),
+                          pack_bf16x2(w[8 * c + 4], w[8 * c + 5]), pack_bf16x2(w[8 * c + 6], w[8 * c + 7]));
+  }
+}
+
+// Dequantize sub-block `sb` (32 weights along K) of row n to fp32.
+template <int QT>
+__device__ __forceinline__ void dequant_sub_f32(const uint8_t* const* planes, int K, int n, int sb, float* w) {
+  RawSub<QT> r;
+  load_raw_sub<QT>(planes, K, n, sb, r);
+  dequant_raw<QT>(r, sb & 7, w);
 }
 
 }  // namespace mlxr

@@ -99,24 +99,27 @@ __global__ void pack_q80_kernel(const uint8_t* __restrict__ src, uint8_t* __rest
 
 // One thread per (row, 32-weight sub-block): 32 outputs.
 template <int QT>
-__global__ void dequant_kernel(PlanePtrs P, int N, int K, void* __restrict__ out, int out_dtype) {
+__global__ void dequant_kernel(PlanePtrs P, int N, int K, void* __restrict__ out, int out_dtype, uint32_t nib) {
   const int nsub = K / 32;
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (size_t)N * nsub) return;
   const int n = (int)(idx / nsub), sb = (int)(idx % nsub);
-  float w[32];
-  dequant_sub_f32<QT>(P.p, K, n, sb, w);
+  RawSub<QT> r;
+  load_raw_sub<QT>(P.p, K, n, sb, r);
   const size_t o = (size_t)n * K + (size_t)sb * 32;
   if (out_dtype == DT_F32) {
+    float w[32];
+    dequant_raw<QT>(r, sb & 7, w);
     float4* dst = (float4*)((float*)out + o);
 #pragma unroll
     for (int i = 0; i < 8; ++i) dst[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
   } else {
+    // the exact routine the MFMA GEMM uses to fill its LDS weight tiles
+    uint4 v[4];
+    dequant_raw_bf16<QT>(r, sb & 7, nib, v);
     uint4* dst = (uint4*)((uint16_t*)out + o);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dst[i] = make_uint4(pack_bf16x2(w[8 * i + 0], w[8 * i + 1]), pack_bf16x2(w[8 * i + 2], w[8 * i + 3]),
-                          pack_bf16x2(w[8 * i + 4], w[8 * i + 5]), pack_bf16x2(w[8 * i + 6], w[8 * i + 7]));
+    for (int i = 0; i < 4; ++i) dst[i] = v[i];
   }
 }
 
@@ -152,11 +155,11 @@ hipError_t launch_dequant(const PackedLayout& L, const uint8_t* packed_dev, void
   const int threads = 256;
   const dim3 grid((unsigned)((total + threads - 1) / threads));
   if (L.qtype == QT_Q4_K)
-    dequant_kernel<QT_Q4_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype);
+    dequant_kernel<QT_Q4_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   else if (L.qtype == QT_Q6_K)
-    dequant_kernel<QT_Q6_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype);
+    dequant_kernel<QT_Q6_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   else
-    dequant_kernel<QT_Q8_0><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype);
+    dequant_kernel<QT_Q8_0><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   return hipGetLastError();
 }
 

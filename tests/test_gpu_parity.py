@@ -160,3 +160,15 @@ def test_gemv_rows_independent_of_batch(cuda):
         if m < 3:
             assert torch.equal(y1[0], y3[m])
         assert orc.normwise_rel_err(y1[0].cpu().numpy(), y64[m].cpu().numpy()) <= 1e-6
+
+
+@pytest.mark.parametrize("qt,M,N,K", [(Q4K, 512, 2048, 1024), (Q4K, 300, 1000, 512), (Q6K, 512, 1536, 768),
+                                      (Q80, 512, 1536, 256)])
+def test_mfma_large_tile_matches_oracle(cuda, qt, M, N, K):
+    """Shapes with enough 256x256 tiles to take the large-tile kernel (ragged M and N too)."""
+    import torch
+    w, pw = _packed(torch, qt, N, K, 111 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 112 + N, cuda)
+    y = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
+    assert orc.normwise_rel_err(y.cpu().numpy(), ref) <= TOL
