@@ -1,15 +1,24 @@
 """Benchmark of the quantized matmul path on one MI355X.
 
 Headline (BASELINE.json metric): Q4_K GEMV at M=1 over the Llama-3-8B projection set
-(q, k, v, o, gate, up, down), reported as whole-step HBM GB/s.  One "step" is the seven
-projections of one decoder layer, back to back on one stream.  The packed weights are
-rotated over enough copies (> 512 MB) that every step reads them from HBM, not from the
-256 MB Infinity Cache.  Also reported: per-projection kernel times from HIP events on the
-launch stream, the bf16-MFMA prefill GEMM at M=2048 (TFLOP/s), and the reference's CPU
-path (dequantize all of W to fp32, then the naive fp32 loop; oracle/ restatement) timed
-on the host.
+(q, k, v, o, gate, up, down), as HBM GB/s.  One "step" is the seven projections of one
+decoder layer in four launches -- q/k/v and gate/up read the same input and run as one
+grouped launch each (mlxr_qgemm_run_grouped), o and down alone -- replayed from a hipGraph.
+Packed weights are rotated over enough copies (> 512 MB) that every step reads them from
+HBM rather than the 256 MB Infinity Cache.  Per-launch durations come from HIP events on
+the launch stream around graphs of back-to-back launches of one kind.  The seven-call
+drop-in step (one q_gemm_dequant per projection) is reported beside it.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-prefill]
+The other BASELINE configurations are reported under "configs":
+  c1  Q8_0 GEMV, TinyLlama-1.1B q_proj (M=1, K=N=2048, fp16)
+  c3  Q4_K skinny GEMM, gate/up/down, M in {8,16,32,64} (GEMV kernel and MFMA kernel)
+  c4  Q4_K prefill GEMM, Llama-3-8B set, M in {512, 2048} (bf16 MFMA)
+  c5  Llama-3-70B layer, Q4_K + Q6_K (v, down), 7 GEMMs in a hipGraph at M=1 and M=256
+The CPU baseline is the reference's CPU path (dequantize all of W to fp32, then the naive
+fp32 loop; restated in oracle/orc.c) on the headline workload, one thread.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--only headline,c1,...]
+                    [--no-cpu] [--calib-copy-mb MB]
 """
 import argparse
 import json
@@ -24,11 +33,15 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-SEED_BASE = 0x4D4C5852
+SEED_BASE = 0x4D4C5852  # + configuration index
+ROTATE_BYTES = 640e6
 
-# Llama-3-8B projections: (name, N = out_features, K = in_features)
 LLAMA3_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
              ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+Q4K, Q6K, Q80 = 3, 4, 2
+LLAMA3_70B = [("q", 8192, 8192, Q4K), ("k", 1024, 8192, Q4K), ("v", 1024, 8192, Q6K), ("o", 8192, 8192, Q4K),
+              ("gate", 28672, 8192, Q4K), ("up", 28672, 8192, Q4K), ("down", 8192, 28672, Q6K)]
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_llama3_8b_m1_traffic.txt")
 
 
 def parse():
@@ -36,11 +49,273 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="headline,c1,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the M=2048 MFMA measurement")
-    ap.add_argument("--prefill-reps", type=int, default=10)
-    ap.add_argument("--rotate-mb", type=int, default=640, help="weight bytes rotated per pass (MB)")
+    ap.add_argument("--skip-dropin", action="store_true",
+                    help="do not time the seven-call drop-in step (profiler runs of the headline kernel)")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="after the headline, run one device copy of this many MB (profiler calibration)")
     return ap.parse_args()
+
+
+class Ctx:
+    def __init__(self, torch, mx):
+        self.torch, self.mx = torch, mx
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.current_stream()
+
+    def act(self, M, K, dtype_code, seed):
+        bits = self.mx.synth_act(M * K, dtype_code, seed)
+        t = self.torch.from_numpy(bits.view(np.int16).reshape(M, K)).to(self.dev)
+        return t.view(self.torch.bfloat16 if dtype_code == self.mx.BF16 else self.torch.float16)
+
+    def event_ms(self, fn, reps):
+        torch = self.torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        for r in range(reps):
+            fn(r)
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    def graph(self, fn):
+        """Capture fn() (library launches on the capture stream) into a CUDA/HIP graph."""
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()  # warm-up outside capture (first-call attribute setup)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        torch.cuda.synchronize()
+        return g
+
+
+def pack_copies(cx, specs, seed0, min_copies=2):
+    """specs: [(name, N, K, qtype)] -> (gguf dict, list of {name: PackedWeight})."""
+    mx = cx.mx
+    gguf = {name: mx.synth_gguf(qt, N, K, seed0 + 16 * i) for i, (name, N, K, qt) in enumerate(specs)}
+    layer = sum(mx.packed_size(qt, N, K) for _, N, K, qt in specs)
+    ncopies = max(min_copies, int(-(-ROTATE_BYTES // layer)))
+    copies = [{name: mx.pack_weights(gguf[name], N, K, qt, device=cx.dev) for name, N, K, qt in specs}
+              for _ in range(ncopies)]
+    cx.torch.cuda.synchronize()
+    return gguf, copies, layer
+
+
+def gemm_bytes(mx, qt, M, N, K, xsz=2, ysz=2):
+    return mx.gguf_size(qt, N, K) + M * K * xsz + M * N * ysz
+
+
+# ------------------------------------------------------------------------------ headline
+
+def run_headline(cx, args, out):
+    mx, torch = cx.mx, cx.torch
+    specs = [(n, N, K, Q4K) for n, N, K in LLAMA3_8B]
+    gguf, copies, layer = pack_copies(cx, specs, SEED_BASE + 1)
+    x = {4096: cx.act(1, 4096, mx.BF16, SEED_BASE + 1001), 14336: cx.act(1, 14336, mx.BF16, SEED_BASE + 1002)}
+    ys = {n: torch.empty((1, N), dtype=torch.bfloat16, device=cx.dev) for n, N, K in LLAMA3_8B}
+    dims = {n: (N, K) for n, N, K in LLAMA3_8B}
+    alg = {n: gemm_bytes(mx, Q4K, 1, N, K) for n, N, K in LLAMA3_8B}
+    step_bytes = sum(alg.values())
+    # one decoder layer = 4 launches: the projections of one input run as one grouped launch
+    LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
+
+    def launch(W, names):
+        K = dims[names[0]][1]
+        if len(names) == 1:
+            n = names[0]
+            mx.q_gemm_dequant(x[K], W[n], 1, dims[n][0], K, Q4K, out=ys[n], path=mx.PATH_GEMV)
+        else:
+            mx.q_gemm_dequant_grouped(x[K], [W[n] for n in names], outs=[ys[n] for n in names])
+
+    def step(W):
+        for _, names in LAUNCHES:
+            launch(W, names)
+
+    def step7(W):
+        for n, N, K in LLAMA3_8B:
+            mx.q_gemm_dequant(x[K], W[n], 1, N, K, Q4K, out=ys[n], path=mx.PATH_GEMV)
+
+    R = 12  # launches per timing graph (rotating weight copies)
+    lbytes = {lname: sum(alg[n] for n in names) for lname, names in LAUNCHES}
+    # per-launch durations: graphs of R back-to-back launches of one kind (no host overhead)
+    kern_us = {}
+    for lname, names in LAUNCHES:
+        g = cx.graph(lambda names=names: [launch(copies[r % len(copies)], names) for r in range(R)])
+        g.replay()
+        torch.cuda.synchronize()
+        kern_us[lname] = 1e3 * cx.event_ms(lambda r: g.replay(), max(args.steps // 2, 5)) / R
+        del g
+    avg_us = float(np.mean(list(kern_us.values())))
+    achieved = (step_bytes / len(LAUNCHES)) / (avg_us * 1e-6) / 1e9
+
+    # the timed step: one layer's launches replayed from a hipGraph, one graph per weight copy
+    graphs = [cx.graph(lambda W=W: step(W)) for W in copies]
+    for c in range(args.warmup):
+        graphs[c % len(graphs)].replay()
+    torch.cuda.synchronize()
+    ms_graph = cx.event_ms(lambda r: graphs[r % len(graphs)].replay(), args.steps)
+    graphs7 = []
+    ms_graph7 = ms_eager7 = grouped_ok = None
+    if not args.skip_dropin:
+        # drop-in path: seven separate q_gemm_dequant calls per layer, graph-replayed and eager
+        graphs7 = [cx.graph(lambda W=W: step7(W)) for W in copies]
+        ms_graph7 = cx.event_ms(lambda r: graphs7[r % len(graphs7)].replay(), args.steps)
+        ms_eager7 = cx.event_ms(lambda r: step7(copies[r % len(copies)]), args.steps)
+        # the grouped graph's outputs equal seven separate calls on the same weights, bit for bit
+        graphs[-1].replay()
+        torch.cuda.synchronize()
+        y_g = {n: ys[n].clone() for n in ys}
+        step7(copies[-1])
+        torch.cuda.synchronize()
+        grouped_ok = all(torch.equal(y_g[n], ys[n]) for n in ys)
+
+    if args.calib_copy_mb:
+        nb = args.calib_copy_mb * 1000000
+        src = torch.empty(nb, dtype=torch.uint8, device=cx.dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = float(line.split(":")[1])
+
+    out.update({
+        "value": round(step_bytes / (ms_graph * 1e-3) / 1e9, 1),
+        "ms_per_step": round(ms_graph, 5),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "qgemv_lds_kernel<Q4_K,bf16,M=1> (4 launches per step: qkv, o, gate_up, down)",
+                     "kernel_avg_us": round(avg_us, 3), "alg_bytes_per_launch": round(step_bytes / len(LAUNCHES))},
+        "headline_detail": {
+            "step_bytes": step_bytes,
+            "launches": {ln: {"us": round(kern_us[ln], 3), "bytes": lbytes[ln],
+                              "GBps": round(lbytes[ln] / (kern_us[ln] * 1e-6) / 1e9, 1),
+                              "frac_hbm": round(lbytes[ln] / (kern_us[ln] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                         for ln, _ in LAUNCHES},
+            "dropin_7_calls_graph_ms": ms_graph7 and round(ms_graph7, 5),
+            "dropin_7_calls_graph_GBps": ms_graph7 and round(step_bytes / (ms_graph7 * 1e-3) / 1e9, 1),
+            "dropin_7_calls_eager_ms": ms_eager7 and round(ms_eager7, 5),
+            "grouped_equals_separate_calls": grouped_ok,
+            "weight_copies_rotated": len(copies), "rotated_MB": round(len(copies) * layer / 1e6, 1)},
+    })
+
+    if not args.no_cpu:
+        from oracle import orc
+        orc.set_threads(1)
+        xf = {k: orc.bf16_bits_to_f32(v.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(1, -1)
+              for k, v in x.items()}
+        runs = []
+        for _ in range(3):
+            t = time.perf_counter()
+            for n, N, K in LLAMA3_8B:
+                orc.eval_cpu(Q4K, 1, N, K, gguf[n], xf[K])
+            runs.append(time.perf_counter() - t)
+        sec = float(np.median(runs))
+        out["cpu_baseline"] = {
+            "value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "the full headline step (Llama-3-8B Q4_K q,k,v,o,gate,up,down at M=1) through the "
+                      "reference eval_cpu restated in oracle/orc.c: fp32 dequant of all of W, then the naive "
+                      "fp32 loop; 1 thread; median of 3 runs",
+            "seconds_per_step": round(sec, 4)}
+    del graphs, graphs7, copies
+    torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------------------------------ other configs
+
+def run_c1(cx, args):
+    mx, torch = cx.mx, cx.torch
+    N = K = 2048
+    _, copies, _ = pack_copies(cx, [("q", N, K, Q80)], SEED_BASE + 0, min_copies=8)
+    x = cx.act(1, K, mx.F16, SEED_BASE + 2001)
+    y = torch.empty((1, N), dtype=torch.float16, device=cx.dev)
+    fn = lambda r: mx.q_gemm_dequant(x, copies[r % len(copies)]["q"], 1, N, K, Q80, out=y, path=mx.PATH_GEMV)
+    for r in range(args.warmup):
+        fn(r)
+    us = 1e3 * cx.event_ms(fn, max(args.steps, 50))
+    b = gemm_bytes(mx, Q80, 1, N, K)
+    return {"shape": "M=1 K=2048 N=2048 Q8_0, x/y fp16", "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
+            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": b}
+
+
+def run_c3(cx, args):
+    mx, torch = cx.mx, cx.torch
+    specs = [(n, N, K, Q4K) for n, N, K in LLAMA3_8B if n in ("gate", "up", "down")]
+    _, copies, _ = pack_copies(cx, specs, SEED_BASE + 2)
+    res = {}
+    for M in (8, 16, 32, 64):
+        x = {4096: cx.act(M, 4096, mx.BF16, SEED_BASE + 3000 + M), 14336: cx.act(M, 14336, mx.BF16, SEED_BASE + 3100 + M)}
+        row = {}
+        for n, N, K, _ in specs:
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev)
+            b = gemm_bytes(mx, Q4K, M, N, K)
+            for path, pname in ((mx.PATH_GEMV, "gemv"), (mx.PATH_MFMA, "mfma")):
+                fn = lambda r: mx.q_gemm_dequant(x[K], copies[r % len(copies)][n], M, N, K, Q4K, out=y, path=path)
+                fn(0)
+                us = 1e3 * cx.event_ms(fn, max(args.steps // 2, 10))
+                row[f"{n}_{pname}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                                       "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        res[f"M={M}"] = row
+    return res
+
+
+def run_c4(cx, args):
+    mx, torch = cx.mx, cx.torch
+    specs = [(n, N, K, Q4K) for n, N, K in LLAMA3_8B]
+    _, copies, _ = pack_copies(cx, specs, SEED_BASE + 3, min_copies=1)
+    W = copies[0]
+    res = {}
+    for M in (512, 2048):
+        x = {4096: cx.act(M, 4096, mx.BF16, SEED_BASE + 4000 + M), 14336: cx.act(M, 14336, mx.BF16, SEED_BASE + 4100 + M)}
+        tot_f = tot_us = 0.0
+        shapes = {}
+        for n, N, K in LLAMA3_8B:
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev)
+            fn = lambda r: mx.q_gemm_dequant(x[K], W[n], M, N, K, Q4K, out=y, path=mx.PATH_MFMA)
+            fn(0)
+            us = 1e3 * cx.event_ms(fn, 5 if M == 2048 else 10)
+            f = 2.0 * M * N * K
+            shapes[n] = {"us": round(us, 1), "TFLOPs": round(f / us / 1e6, 1)}
+            tot_f += f
+            tot_us += us
+        res[f"M={M}"] = {"TFLOPs": round(tot_f / tot_us / 1e6, 1),
+                         "frac_bf16_peak": round(tot_f / tot_us / 1e6 / BF16_PEAK_TFLOPS, 4), "shapes": shapes}
+    return res
+
+
+def run_c5(cx, args):
+    mx, torch = cx.mx, cx.torch
+    _, copies, layer = pack_copies(cx, LLAMA3_70B, SEED_BASE + 4, min_copies=2)
+    res = {"weight_bytes_per_layer": sum(mx.gguf_size(qt, N, K) for _, N, K, qt in LLAMA3_70B)}
+    for M in (1, 256):
+        x = {8192: cx.act(M, 8192, mx.BF16, SEED_BASE + 5000 + M), 28672: cx.act(M, 28672, mx.BF16, SEED_BASE + 5100 + M)}
+        ys = {n: torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev) for n, N, K, qt in LLAMA3_70B}
+
+        def layer_fn(W):
+            for n, N, K, qt in LLAMA3_70B:
+                mx.q_gemm_dequant(x[K], W[n], M, N, K, qt, out=ys[n])  # auto path: GEMV at M=1, MFMA at 256
+        graphs = [cx.graph(lambda W=W: layer_fn(W)) for W in copies]
+        for r in range(2):
+            graphs[r % len(graphs)].replay()
+        torch.cuda.synchronize()
+        ms = cx.event_ms(lambda r: graphs[r % len(graphs)].replay(), 10 if M == 1 else 4)
+        byts = sum(gemm_bytes(mx, qt, M, N, K) for _, N, K, qt in LLAMA3_70B)
+        flops = sum(2.0 * M * N * K for _, N, K, qt in LLAMA3_70B)
+        res[f"M={M}"] = {"ms_per_layer": round(ms, 4), "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
+                         "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+                         "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        del graphs
+    return res
 
 
 def main():
@@ -49,151 +324,33 @@ def main():
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
-
     import torch
     import mlxr_amd as mx
 
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    qt = mx.QuantType.Q4_K
-
-    # ---------------------------------------------------------------- inputs
-    gguf = {}
-    for i, (name, N, K) in enumerate(LLAMA3_8B):
-        gguf[name] = mx.synth_gguf(qt, N, K, SEED_BASE + 1 + 16 * i)
-    layer_bytes = sum(mx.packed_size(qt, N, K) for _, N, K in LLAMA3_8B)
-    ncopies = max(2, -(-args.rotate_mb * 1000000 // layer_bytes))
-    copies = []
-    for c in range(ncopies):
-        copies.append({name: mx.pack_weights(gguf[name], N, K, qt, device=dev) for name, N, K in LLAMA3_8B})
-    torch.cuda.synchronize()
-
-    def act(n, seed, M=1):
-        bits = mx.synth_act(M * n, mx.BF16, seed)
-        return torch.from_numpy(bits.view(np.int16).reshape(M, n)).to(dev).view(torch.bfloat16)
-
-    x_h = act(4096, SEED_BASE + 1001)
-    x_i = act(14336, SEED_BASE + 1002)
-    ys = {name: torch.empty((1, N), dtype=torch.bfloat16, device=dev) for name, N, K in LLAMA3_8B}
-
-    def xin(K):
-        return x_h if K == 4096 else x_i
-
-    # algorithmic bytes: GGUF weight bytes + activations read once + outputs written once
-    alg = {name: mx.gguf_size(qt, N, K) + K * 2 + N * 2 for name, N, K in LLAMA3_8B}
-    step_bytes = sum(alg.values())
-    stream = torch.cuda.current_stream()
-
-    def step(c):
-        W = copies[c % ncopies]
-        for name, N, K in LLAMA3_8B:
-            mx.q_gemm_dequant(xin(K), W[name], 1, N, K, qt, out=ys[name], path=mx.PATH_GEMV, stream=stream)
-
-    # ---------------------------------------------------------------- timed steps
-    for c in range(args.warmup):
-        step(c)
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for c in range(args.steps):
-        step(c)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / args.steps
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
-
-    # ---------------------------------------------------------------- per-kernel HIP events
-    reps = max(args.steps, 10)
-    evs = {name: [] for name, _, _ in LLAMA3_8B}
-    for c in range(reps):
-        W = copies[c % ncopies]
-        for name, N, K in LLAMA3_8B:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            mx.q_gemm_dequant(xin(K), W[name], 1, N, K, qt, out=ys[name], path=mx.PATH_GEMV, stream=stream)
-            b.record(stream)
-            evs[name].append((a, b))
-    torch.cuda.synchronize()
-    kern_us = {name: float(np.mean([a.elapsed_time(b) for a, b in evs[name]]) * 1e3) for name in evs}
-    shapes = {name: {"N": N, "K": K, "us": round(kern_us[name], 3),
-                     "GBps": round(alg[name] / (kern_us[name] * 1e-6) / 1e9, 1),
-                     "frac_hbm": round(alg[name] / (kern_us[name] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-              for name, N, K in LLAMA3_8B}
-    kern_total_us = sum(kern_us.values())
-    achieved = step_bytes / (kern_total_us * 1e-6) / 1e9
-
-    # ---------------------------------------------------------------- prefill MFMA, M=2048
-    prefill = None
-    if not args.no_prefill:
-        M = 2048
-        xp = {4096: act(4096, SEED_BASE + 3001, M), 14336: act(14336, SEED_BASE + 3002, M)}
-        yp = {name: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for name, N, K in LLAMA3_8B}
-        W = copies[0]
-        for name, N, K in LLAMA3_8B:  # warmup
-            mx.q_gemm_dequant(xp[K], W[name], M, N, K, qt, out=yp[name], path=mx.PATH_MFMA, stream=stream)
-        torch.cuda.synchronize()
-        pev = {name: [] for name, _, _ in LLAMA3_8B}
-        for r in range(args.prefill_reps):
-            for name, N, K in LLAMA3_8B:
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-                mx.q_gemm_dequant(xp[K], W[name], M, N, K, qt, out=yp[name], path=mx.PATH_MFMA, stream=stream)
-                b.record(stream)
-                pev[name].append((a, b))
-        torch.cuda.synchronize()
-        p_us = {name: float(np.mean([a.elapsed_time(b) for a, b in pev[name]]) * 1e3) for name in pev}
-        flops = {name: 2.0 * M * N * K for name, N, K in LLAMA3_8B}
-        tot_tf = sum(flops.values()) / (sum(p_us.values()) * 1e-6) / 1e12
-        prefill = {"M": M, "TFLOPs": round(tot_tf, 1), "frac_bf16_peak": round(tot_tf / BF16_PEAK_TFLOPS, 4),
-                   "shapes": {name: {"us": round(p_us[name], 1),
-                                     "TFLOPs": round(flops[name] / (p_us[name] * 1e-6) / 1e12, 1)}
-                              for name, _, _ in LLAMA3_8B}}
-
-    # ---------------------------------------------------------------- CPU baseline (oracle)
-    cpu = None
-    if not args.no_cpu:
-        from oracle import orc
-        orc.set_threads(1)
-        xh = orc.bf16_bits_to_f32(x_h.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(1, -1)
-        xi = orc.bf16_bits_to_f32(x_i.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(1, -1)
-        runs = []
-        for _ in range(3):
-            t = time.perf_counter()
-            for name, N, K in LLAMA3_8B:
-                orc.eval_cpu(int(qt), 1, N, K, gguf[name], xh if K == 4096 else xi)
-            runs.append(time.perf_counter() - t)
-        sec = float(np.median(runs))
-        cpu = {"value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": "full Llama-3-8B Q4_K projection set at M=1 (7 GEMVs), reference eval_cpu restated: "
-                         "fp32 dequant of all of W then naive fp32 loop, 1 thread, median of 3 runs",
-               "seconds_per_step": round(sec, 3)}
-
+    torch.cuda.set_device(0)
+    cx = Ctx(torch, mx)
+    only = set(args.only.split(","))
     out = {
         "metric": "Q4_K qGEMM: HBM GB/s at M=1 (Llama-3-8B projection set)",
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q4_k x bf16 -> fp32 acc -> bf16",
-        "data": "synthetic (BASELINE generator: d,dmin=|N(0,1)|*1e-3, uniform scales/quants; x ~ N(0,1) bf16)",
-        "config": {"workload": "Llama-3-8B q,k,v,o,gate,up,down Q4_K GEMV, M=1, one decoder layer per step",
-                   "M": 1, "weight_copies_rotated": ncopies, "rotated_MB": round(ncopies * layer_bytes / 1e6, 1),
-                   "step_bytes": step_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qgemv_kernel<Q4_K,bf16,M=1>", "kernel_us_per_step": round(kern_total_us, 3)},
-        "shapes": shapes,
-        "prefill_mfma": prefill,
-        "cpu_baseline": cpu,
+        "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k weights x bf16 activations, fp32 accumulate, bf16 out",
+        "data": "synthetic (BASELINE generators: Q4_K d,dmin=|N(0,1)|*1e-3, uniform scales/quants; x ~ N(0,1))",
+        "config": {"workload": "Llama-3-8B q,k,v,o,gate,up,down Q4_K GEMV at M=1, one decoder layer per step: "
+                               "grouped qkv, o, grouped gate_up, down launches replayed from a hipGraph, weights "
+                               "rotated beyond the Infinity Cache", "M": 1},
+        "roofline": None, "cpu_baseline": None,
     }
+    if "headline" in only:
+        run_headline(cx, args, out)
+    configs = {}
+    for key, fn in (("c1_q8_0_gemv_tinyllama", run_c1), ("c3_q4k_skinny", run_c3), ("c4_q4k_prefill", run_c4),
+                    ("c5_llama3_70b_layer_graph", run_c5)):
+        if key.split("_")[0] in only:
+            configs[key] = fn(cx, args)
+            torch.cuda.empty_cache()
+    if configs:
+        out["configs"] = configs
     print(json.dumps(out))
 
 

@@ -117,6 +117,26 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
                       const void* x_dev, int x_dtype, const void* bias_dev, int bias_dtype,
                       void* y_dev, int y_dtype, int M, int path, void* stream);
 
+/* One weight of a grouped call (see mlxr_qgemm_run_grouped). */
+typedef struct mlxr_qgemm_item {
+  int qtype, N, K, group_size; /* as in mlxr_qgemm_run */
+  const void* packed_dev;      /* packed weight [N, K] */
+  const void* bias_dev;        /* [N] or NULL */
+  int bias_dtype;
+  void* y_dev;                 /* [M, N] */
+  int y_dtype;
+} mlxr_qgemm_item;
+
+/* y_i[M, N_i] = X[M, K] . W_i[N_i, K]^T (+ bias_i) for `count` weights that read the same
+ * activations -- the projections of one input, e.g. q/k/v or gate/up of a decoder layer.
+ * Every item must have the same K.  Items of one quant type at M <= 4 run in a single
+ * launch (up to four per launch) that stages X once; other items run as
+ * mlxr_qgemm_run(..., MLXR_PATH_AUTO).  Results equal count separate mlxr_qgemm_run calls
+ * bit for bit.  No counterpart in the reference (its Linear layers call q_gemm_dequant one
+ * projection at a time, core/graph/layers.cpp:86-99); it exists to cut kernel launches. */
+int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
+                           void* stream);
+
 /* Deterministic synthetic inputs with the shapes/distributions of the benchmark
  * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by
  * Box-Muller in double precision.

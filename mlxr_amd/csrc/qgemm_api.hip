@@ -8,6 +8,7 @@
 #include <stdio.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/mlxr_qgemm.h"
 #include "qgemm_internal.h"
@@ -163,6 +164,58 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
   const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= 64);
   const hipError_t e = gemv ? mlxr::launch_gemv(a, (hipStream_t)stream) : mlxr::launch_mfma(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, gemv ? "gemv launch" : "mfma launch");
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
+                           void* stream) {
+  if (count < 0 || (count > 0 && !items)) return fail(MLXR_E_INVALID, "invalid item list");
+  if (count == 0) return MLXR_OK;
+  std::vector<mlxr::RunArgs> a((size_t)count);
+  const int K = items[0].K;
+  for (int i = 0; i < count; ++i) {
+    const mlxr_qgemm_item& it = items[i];
+    if (it.K != K) return fail(MLXR_E_SHAPE, "grouped items must share K (item %d has K=%d, item 0 K=%d)", i, it.K, K);
+    // full validation of each item, exactly as a single call would do it
+    int rc = mlxr_qgemm_run_ex(it.qtype, it.N, it.K, it.group_size, it.packed_dev, x_dev, x_dtype, it.bias_dev,
+                               it.bias_dtype, it.y_dev, it.y_dtype, 0, MLXR_PATH_AUTO, stream);
+    if (rc) return rc;
+    if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
+    if (M > 0 && (!it.packed_dev || !x_dev || !it.y_dev)) return fail(MLXR_E_INVALID, "null buffer (item %d)", i);
+    mlxr::make_layout(it.qtype, it.N, it.K, &a[i].L);
+    a[i].packed = (const uint8_t*)it.packed_dev;
+    a[i].x = x_dev;
+    a[i].x_dtype = x_dtype;
+    a[i].bias = it.bias_dev;
+    a[i].bias_dtype = it.bias_dtype;
+    a[i].y = it.y_dev;
+    a[i].y_dtype = it.y_dtype;
+    a[i].M = M;
+  }
+  if (M == 0) return MLXR_OK;
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<bool> done((size_t)count, false);
+  for (int i = 0; i < count; ++i) {
+    if (done[i]) continue;
+    if (!mlxr::gemv_groupable(a[i])) {
+      const mlxr_qgemm_item& it = items[i];
+      int rc = mlxr_qgemm_run_ex(it.qtype, it.N, it.K, it.group_size, it.packed_dev, x_dev, x_dtype, it.bias_dev,
+                                 it.bias_dtype, it.y_dev, it.y_dtype, M, MLXR_PATH_AUTO, stream);
+      if (rc) return rc;
+      done[i] = true;
+      continue;
+    }
+    // gather up to four groupable items of this quant type into one launch
+    const mlxr::RunArgs* batch[4];
+    int nb = 0;
+    for (int j = i; j < count && nb < 4; ++j)
+      if (!done[j] && a[j].L.qtype == a[i].L.qtype && mlxr::gemv_groupable(a[j])) {
+        batch[nb++] = &a[j];
+        done[j] = true;
+      }
+    const hipError_t e = mlxr::launch_gemv_grouped(batch, nb, s);
+    if (e != hipSuccess) return hip_fail(e, "grouped gemv launch");
+  }
   return MLXR_OK;
 }
 

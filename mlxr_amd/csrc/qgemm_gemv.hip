@@ -382,11 +382,23 @@ __device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t b
   return r;
 }
 
-struct LdsParams {
-  GemvParams g;
+// One weight of a (possibly grouped) launch.  Weights in one launch share K, the quant
+// type and the activations; each owns a contiguous range of wavefronts.
+struct LdsGroup {
+  PlanePtrs P;
   uint32_t psize[4];  // plane sizes in bytes (all < 2^31)
+  void* y;
+  const void* bias;
+  int N, rows_per_wave, wave_start, y_dtype, bias_dtype;
+};
+
+constexpr int MAX_GROUPS = 4;
+
+struct LdsParams {
+  const void* x;
+  int M, K, ngroups;
   uint32_t cmask, cmagic;  // 0x000F000F and the bf16/fp16 magic, passed at run time
-  int rows_per_wave;
+  LdsGroup g[MAX_GROUPS];
 };
 
 template <int QT>
@@ -450,14 +462,21 @@ __device__ __forceinline__ void decode_chunk(const CLoad<QT>& b, int j, uint32_t
 template <int QT, int XT, int MT, int D, bool LIN>
 __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const GemvParams& p = lp.g;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps the loop scalar
-  const int K = p.K, N = p.N, M = p.M;
+  const int K = lp.K, M = lp.M;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nseg = (nsub + 63) >> 6;
-  const int rpw = lp.rows_per_wave;
-  const int r0 = (blockIdx.x * 4 + wave) * rpw;
+  // which weight of the launch this wavefront works on (scalar search)
+  const int gw = blockIdx.x * 4 + wave;
+  int gi = 0;
+#pragma unroll
+  for (int g = 1; g < MAX_GROUPS; ++g)
+    if (g < lp.ngroups && gw >= lp.g[g].wave_start) gi = g;
+  const LdsGroup& G = lp.g[gi];
+  const int N = G.N;
+  const int rpw = G.rows_per_wave;
+  const int r0 = (gw - G.wave_start) * rpw;
   const int r1 = min(r0 + rpw, N);
   const int C = r1 > r0 ? (r1 - r0) * nseg : 0;
   uint4* xs = (uint4*)smem;                                          // [MT][nseg][4][64]
@@ -465,12 +484,12 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
 
   rsrc_t R[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, lp.psize[i]);
+  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(G.P.p[i] ? G.P.p[i] : (const uint8_t*)lp.x, G.psize[i]);
 
   // Activation loads go out first (two padded tasks per thread; padding reads zeros),
   // then the weight prefetch, so the in-order memory counter never makes the LDS staging
   // wait for HBM.
-  const rsrc_t RX = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+  const rsrc_t RX = make_rsrc(lp.x, (uint32_t)M * (uint32_t)K * 2u);
   const int T = MT * nseg * 64;
   auto xoff = [&](int t) -> uint32_t {
     const int m = t / (nseg * 64), sbp = t - m * nseg * 64;
@@ -598,8 +617,8 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   const int orl = lane / MT, om = lane - orl * MT;
   if (orl < r1 - r0 && om < M) {
     float v = res;
-    if (p.bias) v += load_scalar(p.bias, p.bias_dtype, (size_t)(r0 + orl));
-    store_scalar(p.y, p.y_dtype, (size_t)om * N + r0 + orl, v);
+    if (G.bias) v += load_scalar(G.bias, G.bias_dtype, (size_t)(r0 + orl));
+    store_scalar(G.y, G.y_dtype, (size_t)om * N + r0 + orl, v);
   }
 }
 
@@ -635,35 +654,66 @@ int env_int(const char* name, int dflt) {
 
 template <int QT, int XT, int MT, int D>
 hipError_t launch_lds_t(const LdsParams& lp, unsigned grid, hipStream_t s) {
-  if (((lp.g.K >> 5) & 63) == 0)
-    qgemv_lds_kernel<QT, XT, MT, D, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.g.K), s>>>(lp);
+  if (((lp.K >> 5) & 63) == 0)
+    qgemv_lds_kernel<QT, XT, MT, D, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
   else
-    qgemv_lds_kernel<QT, XT, MT, D, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.g.K), s>>>(lp);
+    qgemv_lds_kernel<QT, XT, MT, D, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
   return hipGetLastError();
 }
 
 // Planes addressed with 32-bit buffer offsets: every plane (and x) must stay below 2 GiB.
-bool lds_fits(const GemvParams& p, const PackedLayout& L, int MT) {
+bool lds_fits(int M, int K, const PackedLayout& L, int MT) {
   for (int i = 0; i < L.nplanes; ++i)
     if (L.size[i] >= (1u << 31)) return false;
-  if ((size_t)p.M * p.K * 2 >= (1u << 31)) return false;
-  return lds_bytes(MT, p.K) <= 65536;
+  if ((size_t)M * K * 2 >= (1u << 31)) return false;
+  return lds_bytes(MT, K) <= 65536;
 }
 
-template <int QT, int XT, int MT>
-hipError_t launch_lds(const GemvParams& p, const PackedLayout& L, hipStream_t s) {
+int mt_for(int M) { return M == 1 ? 1 : M <= 2 ? 2 : 4; }
+
+// Fills the launch parameters for `n` weights sharing x; returns the grid size.
+unsigned lds_setup(const RunArgs* const* items, int n, LdsParams& lp) {
+  const RunArgs& a0 = *items[0];
+  const int MT = mt_for(a0.M);
+  lp.x = a0.x;
+  lp.M = a0.M;
+  lp.K = a0.L.K;
+  lp.ngroups = n;
+  lp.cmask = 0x000F000Fu;
+  lp.cmagic = a0.x_dtype == DT_F16 ? 0x64006400u : 0x43004300u;
+  long total_rows = 0;
+  for (int i = 0; i < n; ++i) total_rows += items[i]->L.N;
+  // rows per wavefront: as few as keep ~waves_per_cu wavefronts per CU busy
+  const long target = (long)num_cus() * waves_per_cu_target();
+  int rpw = (int)min((total_rows + target - 1) / target, (long)(64 / MT));  // row results: one per lane
+  if (rpw < 1) rpw = 1;
+  int ws = 0;
+  for (int i = 0; i < n; ++i) {
+    const RunArgs& a = *items[i];
+    LdsGroup& G = lp.g[i];
+    G.P = plane_ptrs(a.L, a.packed);
+    for (int k = 0; k < 4; ++k) G.psize[k] = k < a.L.nplanes ? (uint32_t)a.L.size[k] : 0u;
+    G.y = a.y;
+    G.bias = a.bias;
+    G.N = a.L.N;
+    G.rows_per_wave = rpw;
+    G.wave_start = ws;
+    G.y_dtype = a.y_dtype;
+    G.bias_dtype = a.bias_dtype;
+    ws += (a.L.N + rpw - 1) / rpw;
+  }
+  return (unsigned)((ws + 3) / 4);
+}
+
+template <int QT, int XT>
+hipError_t launch_lds(const RunArgs* const* items, int n, hipStream_t s) {
   static const int depth = env_int("MLXR_GEMV_DEPTH", 3);
   LdsParams lp;
-  lp.g = p;
-  for (int i = 0; i < 4; ++i) lp.psize[i] = i < L.nplanes ? (uint32_t)L.size[i] : 0u;
-  lp.cmask = 0x000F000Fu;
-  lp.cmagic = XT == X_BF16 ? 0x43004300u : 0x64006400u;
-  const int target = num_cus() * waves_per_cu_target();
-  lp.rows_per_wave = min((p.N + target - 1) / target, 64 / MT);  // row results are held one per lane
-  const int waves = (p.N + lp.rows_per_wave - 1) / lp.rows_per_wave;
-  const unsigned grid = (unsigned)((waves + 3) / 4);
-  if (depth >= 4) return launch_lds_t<QT, XT, MT, 4>(lp, grid, s);
-  return launch_lds_t<QT, XT, MT, 3>(lp, grid, s);
+  const unsigned grid = lds_setup(items, n, lp);
+  const int M = lp.M;
+  if (M == 1) return depth >= 4 ? launch_lds_t<QT, XT, 1, 4>(lp, grid, s) : launch_lds_t<QT, XT, 1, 3>(lp, grid, s);
+  if (M == 2) return launch_lds_t<QT, XT, 2, 3>(lp, grid, s);
+  return launch_lds_t<QT, XT, 4, 3>(lp, grid, s);
 }
 
 template <int QT, int XT, int MT, int R>
@@ -675,12 +725,11 @@ hipError_t launch_t(const GemvParams& p, hipStream_t s) {
 }
 
 template <int QT, int XT>
-hipError_t launch_x(const GemvParams& p, const PackedLayout& L, int R, hipStream_t s) {
+hipError_t launch_x(const GemvParams& p, const RunArgs& a, int R, hipStream_t s) {
   const int M = p.M;
-  if (M <= 4 && lds_fits(p, L, M == 1 ? 1 : M <= 2 ? 2 : 4)) {
-    if (M == 1) return launch_lds<QT, XT, 1>(p, L, s);
-    if (M == 2) return launch_lds<QT, XT, 2>(p, L, s);
-    return launch_lds<QT, XT, 4>(p, L, s);
+  if (M <= 4 && lds_fits(M, p.K, a.L, mt_for(M))) {
+    const RunArgs* items[1] = {&a};
+    return launch_lds<QT, XT>(items, 1, s);
   }
   if (M == 1) {
     if (R >= 4) return launch_t<QT, XT, 1, 4>(p, s);
@@ -695,7 +744,7 @@ hipError_t launch_x(const GemvParams& p, const PackedLayout& L, int R, hipStream
   return launch_t<QT, XT, 64, 1>(p, s);
 }
 
-// Rows per wavefront at M = 1: as many as keep >= 16 wavefronts per CU in flight.
+// Rows per wavefront at M = 1 in the register-staged kernel.
 int pick_rows(int N) {
   if (N >= 4 * 4096) return 4;
   if (N >= 2 * 4096) return 2;
@@ -718,9 +767,21 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s) {
   const int R = pick_rows(p.N);
   const bool f16 = a.x_dtype == DT_F16;
   switch (a.L.qtype) {
-    case QT_Q4_K: return f16 ? launch_x<QT_Q4_K, X_F16>(p, a.L, R, s) : launch_x<QT_Q4_K, X_BF16>(p, a.L, R, s);
-    case QT_Q6_K: return f16 ? launch_x<QT_Q6_K, X_F16>(p, a.L, R, s) : launch_x<QT_Q6_K, X_BF16>(p, a.L, R, s);
-    default: return f16 ? launch_x<QT_Q8_0, X_F16>(p, a.L, R, s) : launch_x<QT_Q8_0, X_BF16>(p, a.L, R, s);
+    case QT_Q4_K: return f16 ? launch_x<QT_Q4_K, X_F16>(p, a, R, s) : launch_x<QT_Q4_K, X_BF16>(p, a, R, s);
+    case QT_Q6_K: return f16 ? launch_x<QT_Q6_K, X_F16>(p, a, R, s) : launch_x<QT_Q6_K, X_BF16>(p, a, R, s);
+    default: return f16 ? launch_x<QT_Q8_0, X_F16>(p, a, R, s) : launch_x<QT_Q8_0, X_BF16>(p, a, R, s);
+  }
+}
+
+bool gemv_groupable(const RunArgs& a) { return a.M <= 4 && lds_fits(a.M, a.L.K, a.L, mt_for(a.M)); }
+
+hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s) {
+  const RunArgs& a = *items[0];
+  const bool f16 = a.x_dtype == DT_F16;
+  switch (a.L.qtype) {
+    case QT_Q4_K: return f16 ? launch_lds<QT_Q4_K, X_F16>(items, n, s) : launch_lds<QT_Q4_K, X_BF16>(items, n, s);
+    case QT_Q6_K: return f16 ? launch_lds<QT_Q6_K, X_F16>(items, n, s) : launch_lds<QT_Q6_K, X_BF16>(items, n, s);
+    default: return f16 ? launch_lds<QT_Q8_0, X_F16>(items, n, s) : launch_lds<QT_Q8_0, X_BF16>(items, n, s);
   }
 }
 

@@ -37,6 +37,11 @@ hipError_t launch_dequant(const PackedLayout& L, const uint8_t* packed_dev, void
 // Wavefront-reduction GEMV / skinny GEMM, no MFMA.  Requires 1 <= M <= 64.
 hipError_t launch_gemv(const RunArgs& a, hipStream_t s);
 
+// Several weights that share K, quant type, activations and M (<= 4) in one launch;
+// gemv_groupable() tells whether an item qualifies.  n <= 4.
+bool gemv_groupable(const RunArgs& a);
+hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s);
+
 // LDS-dequant bf16 MFMA GEMM.  Any M >= 1 (rows beyond M are masked).
 hipError_t launch_mfma(const RunArgs& a, hipStream_t s);
 

@@ -39,6 +39,13 @@ class QuantType(enum.IntEnum):
     IQ3_S = 15
 
 
+class Item(ctypes.Structure):
+    """mlxr_qgemm_item."""
+    _fields_ = [("qtype", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int), ("group_size", ctypes.c_int),
+                ("packed_dev", ctypes.c_void_p), ("bias_dev", ctypes.c_void_p), ("bias_dtype", ctypes.c_int),
+                ("y_dev", ctypes.c_void_p), ("y_dtype", ctypes.c_int)]
+
+
 class QGemmError(RuntimeError):
     """A nonzero status from the C ABI; ``code`` holds the MLXR_E_* value."""
 
@@ -61,6 +68,7 @@ _SIGS = {
     "mlxr_qgemm_dequant": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run_ex": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "mlxr_qgemm_run_grouped": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
 }
@@ -227,3 +235,25 @@ def q_gemm_dequant(input, weights, M, N, K, quant_type, group_size=0, bias=None,
                                    _dt_code(bias.dtype) if bias is not None else F32, out.data_ptr(),
                                    _dt_code(out.dtype), M, path, _stream_ptr(stream)))
     return out
+
+
+def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=None, stream=None):
+    """y_i = input . W_i^T (+ bias_i) for packed weights that read the same input (e.g. the
+    q/k/v or gate/up projections), in as few launches as the library can (one per four
+    same-type weights at M <= 4).  Returns the list of outputs."""
+    torch = _torch()
+    M, K = input.shape
+    if not input.is_contiguous():
+        input = input.contiguous()
+    n = len(weights)
+    biases = biases or [None] * n
+    if outs is None:
+        outs = [torch.empty((M, w.N), dtype=out_dtype or input.dtype, device=input.device) for w in weights]
+    arr = (Item * n)()
+    for i, (w, y, b) in enumerate(zip(weights, outs, biases)):
+        if w.K != K:
+            raise QGemmError(-3, "Input shape must be [M, K]")
+        arr[i] = Item(int(w.qtype), w.N, w.K, 0, w.data_ptr(), b.data_ptr() if b is not None else None,
+                      _dt_code(b.dtype) if b is not None else F32, y.data_ptr(), _dt_code(y.dtype))
+    _check(lib().mlxr_qgemm_run_grouped(n, arr, input.data_ptr(), _dt_code(input.dtype), M, _stream_ptr(stream)))
+    return outs

@@ -172,3 +172,24 @@ def test_mfma_large_tile_matches_oracle(cuda, qt, M, N, K):
     y = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
     assert orc.normwise_rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_grouped_equals_separate_calls(cuda, M):
+    """q/k/v-style projections of one input: the grouped call (one launch per four
+    same-type weights at M <= 4, separate launches otherwise) equals separate calls bit for
+    bit, including a mixed-type group and a bias."""
+    import torch
+    K = 1024
+    specs = [(Q4K, 512), (Q4K, 128), (Q6K, 128), (Q4K, 640), (Q4K, 256)]
+    ws = [mx.pack_weights(mx.synth_gguf(qt, N, K, 200 + i), N, K, qt, device=cuda) for i, (qt, N) in enumerate(specs)]
+    x, xf = _act(torch, M, K, mx.BF16, 210, cuda)
+    bias = torch.linspace(-1, 1, 128, device=cuda).to(torch.bfloat16)
+    biases = [None, bias, None, None, None]
+    ys = mx.q_gemm_dequant_grouped(x, ws, biases=biases, out_dtype=torch.float32)
+    for i, (w, y) in enumerate(zip(ws, ys)):
+        y1 = mx.q_gemm_dequant(x, w, M, w.N, K, w.qtype, bias=biases[i], out_dtype=torch.float32)
+        assert torch.equal(y, y1), i
+        ref = orc.gemm_f64(int(w.qtype), M, w.N, K, mx.synth_gguf(w.qtype, w.N, K, 200 + i), xf,
+                           bias=None if biases[i] is None else biases[i].float().cpu().numpy())
+        assert orc.normwise_rel_err(y.cpu().numpy(), ref) <= TOL
