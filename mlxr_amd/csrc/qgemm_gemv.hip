@@ -473,7 +473,26 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
 #pragma unroll
   for (int g = 1; g < MAX_GROUPS; ++g)
     if (g < lp.ngroups && gw >= lp.g[g].wave_start) gi = g;
-  const LdsGroup& G = lp.g[gi];
+  // select the group's fields with static kernarg offsets, so every parameter load is
+  // issued at once instead of after the (scalar) search
+  LdsGroup G = lp.g[0];
+#pragma unroll
+  for (int g = 1; g < MAX_GROUPS; ++g) {
+    const LdsGroup& H = lp.g[g];
+    const bool t = g == gi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      G.P.p[i] = t ? H.P.p[i] : G.P.p[i];
+      G.psize[i] = t ? H.psize[i] : G.psize[i];
+    }
+    G.y = t ? H.y : G.y;
+    G.bias = t ? H.bias : G.bias;
+    G.N = t ? H.N : G.N;
+    G.rows_per_wave = t ? H.rows_per_wave : G.rows_per_wave;
+    G.wave_start = t ? H.wave_start : G.wave_start;
+    G.y_dtype = t ? H.y_dtype : G.y_dtype;
+    G.bias_dtype = t ? H.bias_dtype : G.bias_dtype;
+  }
   const int N = G.N;
   const int rpw = G.rows_per_wave;
   const int r0 = (gw - G.wave_start) * rpw;
@@ -622,6 +641,7 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   }
 }
 
+
 size_t lds_bytes(int MT, int K) { return (size_t)MT * (size_t)(((K >> 5) + 63) >> 6) * 64 * 72; }
 
 int num_cus() {
@@ -704,6 +724,7 @@ unsigned lds_setup(const RunArgs* const* items, int n, LdsParams& lp) {
   }
   return (unsigned)((ws + 3) / 4);
 }
+
 
 template <int QT, int XT>
 hipError_t launch_lds(const RunArgs* const* items, int n, hipStream_t s) {

@@ -410,6 +410,8 @@ hipError_t launch_t(MfmaParams p, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
+  static const int use_tile = getenv("MLXR_MFMA_OLD") ? 0 : 1;
+  if (use_tile && tile_fits(a)) return launch_tile(a, s);
   MfmaParams p;
   p.P = plane_ptrs(a.L, a.packed);
   p.x = a.x;
