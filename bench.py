@@ -89,7 +89,7 @@ class Ctx:
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=s):  # the warm-up stream (per-stream split-K workspace)
             fn()
         torch.cuda.synchronize()
         return g

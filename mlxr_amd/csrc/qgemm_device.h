@@ -104,23 +104,6 @@ __device__ __forceinline__ void load_raw_sub(const uint8_t* const* planes, int K
   }
 }
 
-template <int QT>
-__device__ __forceinline__ void zero_raw_sub(RawSub<QT>& r) {
-  if constexpr (QT == QT_Q4_K) {
-    r.q = make_uint4(0, 0, 0, 0);
-    r.h = make_uint4(0, 0, 0, 0);
-  } else if constexpr (QT == QT_Q6_K) {
-    r.ql = make_uint4(0, 0, 0, 0);
-    r.qh = make_uint2(0, 0);
-    r.sc = 0;
-    r.d = 0;
-  } else {
-    r.a = make_uint4(0, 0, 0, 0);
-    r.b = make_uint4(0, 0, 0, 0);
-    r.d = 0;
-  }
-}
-
 // fp32 weights of one sub-block, exactly as the GGUF formulas define (every product
 // below is exact in fp32; Q4_K rounds once, in the fma).  j = sub-block index within its
 // super-block (sb % 8).
@@ -158,58 +141,6 @@ __device__ __forceinline__ void dequant_raw(const RawSub<QT>& r, int j, float* w
       w[e] = (float)v * d;
     }
   }
-}
-
-// The same weights rounded to bf16 (RNE) and packed in K order: out[c] holds weights
-// 8c..8c+7.  `nib` must be 0x0F0F0F0F; it is passed at run time so the compiler keeps the
-// byte-select converts (v_cvt_f32_ubyte0..3) instead of folding them into bit-field
-// extracts.  Every fp32 value is the same single-rounded fma as dequant_raw.
-template <int QT>
-__device__ __forceinline__ void dequant_raw_bf16(const RawSub<QT>& r, int j, uint32_t nib, uint4* out) {
-  if constexpr (QT == QT_Q4_K) {
-    const uint32_t dd = q4k_dd(r.h);
-    const uint32_t hw[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
-    const uint32_t f = (hw[j >> 1] >> (16 * (j & 1))) & 0xfffu;
-    const float dsc = f16_bits_to_f32(dd & 0xffffu) * (float)(f & 63u);
-    const float ndm = -(f16_bits_to_f32(dd >> 16) * (float)(f >> 6));
-    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-    uint32_t o[16];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      // pair-interleaved word: bytes of (w & nib) are weights 0, 4, 1, 5 of the word,
-      // bytes of ((w >> 4) & nib) are weights 2, 6, 3, 7
-      const uint32_t lo = qw[t] & nib, hi = (qw[t] >> 4) & nib;
-      const float e0 = __builtin_fmaf(dsc, (float)(lo & 0xffu), ndm);
-      const float e4 = __builtin_fmaf(dsc, (float)((lo >> 8) & 0xffu), ndm);
-      const float e1 = __builtin_fmaf(dsc, (float)((lo >> 16) & 0xffu), ndm);
-      const float e5 = __builtin_fmaf(dsc, (float)(lo >> 24), ndm);
-      const float e2 = __builtin_fmaf(dsc, (float)(hi & 0xffu), ndm);
-      const float e6 = __builtin_fmaf(dsc, (float)((hi >> 8) & 0xffu), ndm);
-      const float e3 = __builtin_fmaf(dsc, (float)((hi >> 16) & 0xffu), ndm);
-      const float e7 = __builtin_fmaf(dsc, (float)(hi >> 24), ndm);
-      o[4 * t + 0] = pack_bf16x2(e0, e1);
-      o[4 * t + 1] = pack_bf16x2(e2, e3);
-      o[4 * t + 2] = pack_bf16x2(e4, e5);
-      o[4 * t + 3] = pack_bf16x2(e6, e7);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) out[c] = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
-  } else {
-    float w[32];
-    dequant_raw<QT>(r, j, w);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      out[c] = make_uint4(pack_bf16x2(w[8 * c + 0], w[8 * c + 1]), pack_bf16x2(w[8 * c + 2], w[8 * c + 3]),
-                          pack_bf16x2(w[8 * c + 4], w[8 * c + 5]), pack_bf16x2(w[8 * c + 6], w[8 * c + 7]));
-  }
-}
-
-// Dequantize sub-block `sb` (32 weights along K) of row n to fp32.
-template <int QT>
-__device__ __forceinline__ void dequant_sub_f32(const uint8_t* const* planes, int K, int n, int sb, float* w) {
-  RawSub<QT> r;
-  load_raw_sub<QT>(planes, K, n, sb, r);
-  dequant_raw<QT>(r, sb & 7, w);
 }
 
 }  // namespace mlxr

@@ -42,12 +42,7 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s);
 bool gemv_groupable(const RunArgs& a);
 hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s);
 
-// LDS-dequant bf16 MFMA GEMM.  Any M >= 1 (rows beyond M are masked).
+// MFMA GEMM (qgemm_tile.hip).  Any M >= 1 (rows beyond M are masked).
 hipError_t launch_mfma(const RunArgs& a, hipStream_t s);
-
-// Register-dequant MFMA GEMM, 256 x 256 tiles (qgemm_tile.hip).  tile_fits() tells
-// whether the 32-bit buffer offsets cover the operands.
-bool tile_fits(const RunArgs& a);
-hipError_t launch_tile(const RunArgs& a, hipStream_t s);
 
 }  // namespace mlxr

@@ -6,6 +6,7 @@
 // dequant routines at q_gemm_dequant_primitive.mm:189-225.
 #include "qgemm_device.h"
 #include "qgemm_internal.h"
+#include "qgemm_wdequant.h"
 
 namespace mlxr {
 
@@ -114,9 +115,9 @@ __global__ void dequant_kernel(PlanePtrs P, int N, int K, void* __restrict__ out
 #pragma unroll
     for (int i = 0; i < 8; ++i) dst[i] = make_float4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
   } else {
-    // the exact routine the MFMA GEMM uses to fill its LDS weight tiles
+    // the routine the MFMA GEMM uses to build its weight operands
     uint4 v[4];
-    dequant_raw_bf16<QT>(r, sb & 7, nib, v);
+    dequant_sub_words<QT, X_BF16>(P, K, n, sb, nib, v);
     uint4* dst = (uint4*)((uint16_t*)out + o);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dst[i] = v[i];

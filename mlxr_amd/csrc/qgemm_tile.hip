@@ -4,34 +4,42 @@
 // reference (tile loop :374-464: X tile to shared memory, W tile dequantized, fp32
 // accumulation, bias + store :467-485).
 //
-// Tile: 256 (M) x 256 (N) per workgroup, K in steps of 64, four wavefronts; wavefront w
-// owns the 256 x 64 slab of output columns [64w, 64w + 64) as 8 x 2 accumulators of the
-// 32x32x16 MFMA (256 fp32 per lane, in AGPRs).
+// Tile: BM (256 or 128) rows of M x 256 columns of N per workgroup, K in steps of 64,
+// four wavefronts; wavefront w owns the BM x 64 slab of output columns [64w, 64w + 64) as
+// MI x 2 accumulators of the 32x32x16 MFMA (MI = BM/32; in AGPRs).  The 128-row tile
+// doubles the tile count for shapes whose 256-row tiles would leave CUs idle.
 //
 //  * Activations (shared by the four wavefronts) go HBM -> LDS by buffer_load ... lds
-//    (no VGPR staging), four stages, three steps ahead.  A 256 x 64 stage is 32 KiB: row
-//    r is 128 B, its 16-byte chunk c stored at position c ^ (r & 7), so the fragment
-//    reads of eight consecutive rows hit eight different 16-byte bank groups.  The DMA is
-//    issued from inline assembly, so the compiler (which would otherwise wait for every
-//    outstanding load before each LDS read) leaves the waits to the exact vmcnt below.
+//    (no VGPR staging), four stages, three steps ahead.  A BM x 64 stage has 128-byte
+//    rows; the 16-byte chunk c of row r is stored at position c ^ (r & 7), so the
+//    fragment reads of eight consecutive rows hit eight different 16-byte bank groups.
+//    The DMA and the weight loads are issued from inline assembly, so the compiler
+//    (which would otherwise wait for every outstanding load before each LDS read) leaves
+//    all memory waits to the exact vmcnt values computed from the fixed issue order.
 //  * Weights never pass through LDS.  K is permuted inside each 64-step so that in MFMA
 //    kk (0..3) lane half h supplies K positions 32h + 8kk .. +7 for both operands: lane
 //    (n, h) then owns exactly sub-block h of the step for its weight rows n and n + 32,
 //    dequantizes those 32 weights in registers and uses word kk of the result as the B
 //    fragment of MFMA kk.  Per-super-block header work (d, dmin, six-bit scales) is done
 //    once per four steps.  The raw sub-blocks are loaded four steps ahead; the dequant
-//    of step k+1 runs between the MFMAs of step k.
-//  * One barrier per step: a stage is refilled only after every wavefront has left it.
+//    of step k+1 is spread over the MFMAs of step k, a few VALU ops per MFMA.
+//  * One barrier per step, half way through it: the next stage is then complete and the
+//    previous one free for the DMA three steps ahead.
+//  * The MFMAs take the weights as the first operand, so each lane's accumulators hold
+//    four consecutive output columns: the epilogue stores 8 or 16 bytes per access.
 //
 // The dequantized values are the exact GGUF fp32 weights rounded to nearest-even bf16
-// (fp16 for fp16 activations, which use the fp16 MFMA); the same routine backs
-// mlxr_qgemm_dequant, so they are covered by its bit-exact tests.
+// (fp16 for fp16 activations, which use the fp16 MFMA), from the routines of
+// qgemm_wdequant.h, which also back mlxr_qgemm_dequant: its bit-exact tests cover them.
 #include <stdlib.h>
 
+#include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "qgemm_device.h"
 #include "qgemm_internal.h"
+#include "qgemm_wdequant.h"
 
 namespace mlxr {
 
@@ -40,28 +48,12 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
-typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
-typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr uint32_t OOB = 0x80000000u;  // voffset beyond every buffer: loads return 0
-constexpr int TM = 256, TN = 256, TK = 64;
-constexpr int NSTAGE = 4;
-constexpr int A_STAGE = TM * TK * 2;  // bytes
-constexpr int PD = 4;                 // raw weight prefetch distance (steps)
-constexpr int TILE_LDS = NSTAGE * A_STAGE;
-
-enum XType : int { X_BF16 = 0, X_F16 = 1 };
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* ptr, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
+constexpr int TN = 256, TK = 64;
+constexpr int NSTAGE = 4;              // activation stages (DMA three steps ahead)
+constexpr int PD = 4;                  // raw weight prefetch distance (steps)
 
 struct TileParams {
   const void* x;
@@ -70,23 +62,11 @@ struct TileParams {
   const uint8_t* P[4];
   uint32_t psize[4];
   int M, N, K;
+  int ldy;  // row stride of y in elements
   int bias_dtype, y_dtype;
   int tiles_m, tiles_n;
   uint32_t nib;  // 0x0F0F0F0F, passed at run time (keeps the byte converts)
 };
-
-// Two floats -> packed pair of the MFMA element type, round to nearest even.
-template <int XT>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  if constexpr (XT == X_BF16) {
-    return pack_bf16x2(lo, hi);
-  } else {
-    const f32x2_t v = {lo, hi};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
-  }
-}
-
-// ---- per-quant-type raw sub-block, header state and dequant --------------------------
 
 // Loads from inline assembly: the compiler neither sees nor waits for them; every wait
 // is an explicit s_waitcnt vmcnt(n) computed from the fixed issue order, followed by
@@ -112,55 +92,6 @@ __device__ __forceinline__ uint32_t vload_u16(const i32x4_t& r, uint32_t voff) {
   asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=&v"(v) : "v"(voff), "s"(r));
   return v;
 }
-template <typename T>
-__device__ __forceinline__ void pin(T& v) {
-  asm volatile("" : "+v"(v));
-}
-
-template <int QT>
-struct Raw;
-template <>
-struct Raw<QT_Q4_K> {
-  u32x4_t q;
-  __device__ void pin_all() { pin(q); }
-};
-template <>
-struct Raw<QT_Q6_K> {
-  u32x4_t ql;
-  u32x2_t qh;
-  __device__ void pin_all() {
-    pin(ql);
-    pin(qh);
-  }
-};
-template <>
-struct Raw<QT_Q8_0> {
-  u32x4_t a, b;
-  uint32_t d;
-  __device__ void pin_all() {
-    pin(a);
-    pin(b);
-    pin(d);
-  }
-};
-
-// Header bytes of one super-block as loaded; decoded once per four steps.
-template <int QT>
-struct Hdr {
-  u32x4_t h;   // Q4_K: 8 x u16 lane-sliced entries; Q6_K: 16 int8 scales
-  uint32_t d;  // Q6_K: fp16 d
-  __device__ void pin_all() {
-    pin(h);
-    if constexpr (QT == QT_Q6_K) pin(d);
-  }
-};
-// Decoded per-sub-block factors for the four sub-blocks (h, h+2, h+4, h+6) a lane owns
-// in the current super-block.
-template <int QT>
-struct Scales {
-  float a[4], b[4];  // Q4_K: d*sc, -(dmin*m).  Q6_K: d*sc of the two 16-weight groups.
-};
-
 // VMEM instructions of one step's raw loads (two weight rows), and of its header loads.
 template <int QT>
 constexpr int raw_loads() { return QT == QT_Q4_K ? 2 : QT == QT_Q6_K ? 4 : 6; }
@@ -196,143 +127,6 @@ __device__ __forceinline__ void load_hdr(const i32x4_t* R, uint32_t row_sb, int 
   }
 }
 
-template <int QT>
-__device__ __forceinline__ void decode_hdr(const Hdr<QT>& h, int half, Scales<QT>& s) {
-  if constexpr (QT == QT_Q4_K) {
-    const uint32_t dd = q4k_dd(make_uint4(h.h[0], h.h[1], h.h[2], h.h[3]));
-    const float d = f16_bits_to_f32(dd & 0xffffu), dmin = f16_bits_to_f32(dd >> 16);
-    const uint32_t w[4] = {h.h[0], h.h[1], h.h[2], h.h[3]};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      // entry j = 2q + half sits in word q, half `half`
-      const uint32_t f = (half ? (w[q] >> 16) : w[q]) & 0xfffu;
-      s.a[q] = d * (float)(f & 63u);
-      s.b[q] = -(dmin * (float)(f >> 6));
-    }
-  } else if constexpr (QT == QT_Q6_K) {
-    const float d = f16_bits_to_f32(h.d & 0xffffu);
-    const uint32_t w[4] = {h.h[0], h.h[1], h.h[2], h.h[3]};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      // sub-block j = 2q + half uses scales 2j, 2j + 1: bytes 4q + 2half, +1 = word q
-      const uint32_t v = half ? (w[q] >> 16) : w[q];
-      s.a[q] = d * (float)(int8_t)(v & 0xffu);
-      s.b[q] = d * (float)(int8_t)((v >> 8) & 0xffu);
-    }
-  }
-}
-
-// B fragment kk of one sub-block: its weights 8kk .. 8kk+7, rounded to the MFMA type.
-template <int QT, int XT, int kk>
-__device__ __forceinline__ uint4 dequant_word(const Raw<QT>& r, const Scales<QT>& s, int q, uint32_t nib) {
-  if constexpr (QT == QT_Q4_K) {
-    const float a = s.a[q], b = s.b[q];
-    uint32_t w = r.q[kk];
-    pin(w);  // keeps this work at its place in the MFMA stream
-    // pair-interleaved word: bytes of (w & nib) are weights 0, 4, 1, 5; of ((w >> 4) & nib) 2, 6, 3, 7
-    const uint32_t lo = w & nib, hi = (w >> 4) & nib;
-    const float e0 = __builtin_fmaf(a, (float)(lo & 0xffu), b);
-    const float e4 = __builtin_fmaf(a, (float)((lo >> 8) & 0xffu), b);
-    const float e1 = __builtin_fmaf(a, (float)((lo >> 16) & 0xffu), b);
-    const float e5 = __builtin_fmaf(a, (float)(lo >> 24), b);
-    const float e2 = __builtin_fmaf(a, (float)(hi & 0xffu), b);
-    const float e6 = __builtin_fmaf(a, (float)((hi >> 8) & 0xffu), b);
-    const float e3 = __builtin_fmaf(a, (float)((hi >> 16) & 0xffu), b);
-    const float e7 = __builtin_fmaf(a, (float)(hi >> 24), b);
-    return make_uint4(pack2<XT>(e0, e1), pack2<XT>(e2, e3), pack2<XT>(e4, e5), pack2<XT>(e6, e7));
-  } else if constexpr (QT == QT_Q6_K) {
-    // weights 8kk .. 8kk+7: group 0 (scale a) for kk < 2, group 1 (scale b) otherwise;
-    // value d*sc*(q - 32) = fma(d*sc, q, -32*d*sc), exact
-    const float a = (kk < 2) ? s.a[q] : s.b[q];
-    const float c = -32.f * a;
-    uint32_t lw = r.ql[kk];
-    uint32_t hv = r.qh[kk >> 1];
-    pin(lw);  // keeps this work at its place in the MFMA stream
-    pin(hv);
-    uint32_t o[4];
-#pragma unroll
-    for (int sp = 0; sp < 4; ++sp) {
-      const int rs = 8 * (kk & 1) + 2 * sp - 4;
-      const uint32_t hs = rs >= 0 ? (hv >> rs) : (hv << (-rs));
-      const uint32_t v = ((lw >> (4 * sp)) & (nib & 0x000F000Fu)) | (hs & 0x00300030u);
-      o[sp] = pack2<XT>(__builtin_fmaf(a, (float)(v & 0xffu), c), __builtin_fmaf(a, (float)((v >> 16) & 0xffu), c));
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
-  } else {
-    // int8 q -> (q + 128) by flipping the sign bits; q*d = fma(d, q + 128, -128 d), exact
-    const float d = f16_bits_to_f32(r.d & 0xffffu), c = -128.f * d;
-    const uint32_t w0 = kk < 2 ? r.a[2 * kk] : r.b[2 * kk - 4];
-    const uint32_t w1 = kk < 2 ? r.a[2 * kk + 1] : r.b[2 * kk - 3];
-    uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
-    pin(u0);  // keeps this work at its place in the MFMA stream
-    pin(u1);
-    return make_uint4(pack2<XT>(__builtin_fmaf(d, (float)(u0 & 0xffu), c), __builtin_fmaf(d, (float)((u0 >> 8) & 0xffu), c)),
-                      pack2<XT>(__builtin_fmaf(d, (float)((u0 >> 16) & 0xffu), c), __builtin_fmaf(d, (float)(u0 >> 24), c)),
-                      pack2<XT>(__builtin_fmaf(d, (float)(u1 & 0xffu), c), __builtin_fmaf(d, (float)((u1 >> 8) & 0xffu), c)),
-                      pack2<XT>(__builtin_fmaf(d, (float)((u1 >> 16) & 0xffu), c), __builtin_fmaf(d, (float)(u1 >> 24), c)));
-  }
-}
-
-// The same dequant split into a prelude and four quarter tasks (one bf16/fp16 pair
-// each), so the work can be spread one task per MFMA.  Quarter order matches
-// dequant_word: pairs (0,1), (2,3), (4,5), (6,7) of the word.
-template <int QT>
-struct WordTmp {
-  uint32_t u0, u1;
-  float a, c;
-};
-
-template <int QT, int kk>
-__device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>& s, int q, uint32_t nib,
-                                             WordTmp<QT>& t) {
-  if constexpr (QT == QT_Q4_K) {
-    uint32_t w = r.q[kk];
-    pin(w);
-    t.u0 = w & nib;
-    t.u1 = (w >> 4) & nib;
-    t.a = s.a[q];
-    t.c = s.b[q];
-  } else if constexpr (QT == QT_Q6_K) {
-    uint32_t lw = r.ql[kk], hv = r.qh[kk >> 1];
-    pin(lw);
-    pin(hv);
-    t.u0 = lw;
-    t.u1 = hv;
-    t.a = (kk < 2) ? s.a[q] : s.b[q];
-    t.c = -32.f * t.a;
-  } else {
-    uint32_t w0 = kk < 2 ? r.a[2 * kk] : r.b[2 * kk - 4];
-    uint32_t w1 = kk < 2 ? r.a[2 * kk + 1] : r.b[2 * kk - 3];
-    pin(w0);
-    pin(w1);
-    t.u0 = w0 ^ 0x80808080u;
-    t.u1 = w1 ^ 0x80808080u;
-    t.a = f16_bits_to_f32(r.d & 0xffffu);
-    t.c = -128.f * t.a;
-  }
-}
-
-template <int QT, int XT, int kk, int qq>
-__device__ __forceinline__ uint32_t word_quarter(const WordTmp<QT>& t, uint32_t nib) {
-  if constexpr (QT == QT_Q4_K) {
-    // u0 bytes: weights 0, 4, 1, 5; u1 bytes: 2, 6, 3, 7
-    const uint32_t v = (qq & 1) ? t.u1 : t.u0;
-    const int sh = (qq & 2) ? 8 : 0;
-    return pack2<XT>(__builtin_fmaf(t.a, (float)((v >> sh) & 0xffu), t.c),
-                     __builtin_fmaf(t.a, (float)((v >> (16 + sh)) & 0xffu), t.c));
-  } else if constexpr (QT == QT_Q6_K) {
-    constexpr int rs = 8 * (kk & 1) + 2 * qq - 4;
-    const uint32_t hs = rs >= 0 ? (t.u1 >> rs) : (t.u1 << (-rs));
-    const uint32_t v = ((t.u0 >> (4 * qq)) & (nib & 0x000F000Fu)) | (hs & 0x00300030u);
-    return pack2<XT>(__builtin_fmaf(t.a, (float)(v & 0xffu), t.c), __builtin_fmaf(t.a, (float)((v >> 16) & 0xffu), t.c));
-  } else {
-    const uint32_t v = (qq < 2) ? t.u0 : t.u1;
-    const int sh = (qq & 1) ? 16 : 0;
-    return pack2<XT>(__builtin_fmaf(t.a, (float)((v >> sh) & 0xffu), t.c),
-                     __builtin_fmaf(t.a, (float)((v >> (sh + 8)) & 0xffu), t.c));
-  }
-}
-
 template <int XT>
 __device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f32x16_t& c) {
   if constexpr (XT == X_BF16)
@@ -353,14 +147,13 @@ __device__ __forceinline__ void sfor(Fn&& fn) {
   sfor_impl(fn, std::make_integer_sequence<int, N>());
 }
 
-#define SCHED_MFMA(n) __builtin_amdgcn_sched_group_barrier(0x008, n, 0)
-#define SCHED_VALU(n) __builtin_amdgcn_sched_group_barrier(0x002, n, 0)
-#define SCHED_DSR(n) __builtin_amdgcn_sched_group_barrier(0x100, n, 0)
-#define SCHED_VMEM(n) __builtin_amdgcn_sched_group_barrier(0x020, n, 0)
-#define SCHED_DSW(n) __builtin_amdgcn_sched_group_barrier(0x200, n, 0)
-
-template <int QT, int XT>
+template <int QT, int XT, int MI>
 __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
+  constexpr int BM = 32 * MI;              // tile rows (M)
+  constexpr int A_STAGE = BM * TK * 2;     // bytes per activation stage
+  constexpr int NF = 4 * MI;               // A fragments per step
+  constexpr int NSLOT = 2 * NF;            // MFMAs per step
+  constexpr int SPS = NSLOT / 4;           // MFMA slots per slice kk
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -372,7 +165,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   int t = b;
   if ((ntiles & 7) == 0) t = (b & 7) * (ntiles >> 3) + (b >> 3);
   const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
-  const int m0 = tm * TM, n0 = tn * TN;
+  const int m0 = tm * BM, n0 = tn * TN;
   const int M = p.M, N = p.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK - 1) / TK;
@@ -390,35 +183,39 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) R[i] = srsrc(p.P[i] ? p.P[i] : (const uint8_t*)p.x, p.psize[i]);
 
-  // --- activations: LDS DMA.  Wave w fills slot blocks 8w .. 8w+7 of a stage (1 KiB =
-  // 8 rows each); lane l of block b brings row 8b + l/8, global chunk (l%8) ^ (l/8), to
-  // chunk position l%8.  Rows past M read zeros.
-  uint32_t a_voff[8];
-  const int a_pos = lane & 7;
-  const int a_c = a_pos ^ (lane >> 3);
+  // --- activations: LDS DMA.  Wave w fills slot blocks MI*w .. MI*w+MI-1 of a stage
+  // (1 KiB = 8 rows each); lane l of block b brings row 8b + l/8, global chunk
+  // (l%8) ^ (l/8), to chunk position l%8.  Rows past M read zeros.
+  uint32_t a_voff[MI];
+  const int a_c = (lane & 7) ^ (lane >> 3);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 8 * (8 * wave + i) + (lane >> 3);
+  for (int i = 0; i < MI; ++i) {
+    const int r = 8 * (MI * wave + i) + (lane >> 3);
     a_voff[i] = (m0 + r < M) ? ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)a_c * 8u) * 2u : OOB;
   }
   const int ktail = K % TK;  // only Q8_0 can end on a half step (32 of 64)
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
   const i32x4_t rx = srsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
-  // Always eight DMA instructions per wavefront and step (steps past the end read
-  // zeros into a stage nobody reads), so the wait counts below are exact.
+  // Always MI DMA instructions per wavefront and step (steps past the end read zeros
+  // into a stage nobody reads), so the wait counts below are exact.
   auto issue_a = [&](int kt) {
     const bool live = kt < nkt;
     const bool cut = ktail != 0 && kt == nkt - 1 && a_c * 8 >= ktail;
     const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane(kt * (TK * 2));
-    const uint32_t dst = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * A_STAGE + wave * 8 * 1024);
+    const uint32_t dst = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * A_STAGE + wave * MI * 1024);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < MI; ++i) {
       const uint32_t vo = (live && !cut) ? a_voff[i] : OOB;
       const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + i * 1024));
+      // M0 holds the LDS destination; nothing else in this kernel uses M0 (DS
+      // instructions on gfx9+ do not), so clobbering it is safe here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
       asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                    :
                    : "v"(vo), "s"(rx), "s"(soff), "s"(m0v)
                    : "memory", "m0");
+#pragma clang diagnostic pop
     }
   };
 
@@ -456,8 +253,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   constexpr int RB = raw_loads<QT>(), RH = hdr_loads<QT>();
   auto rops = [](int slot) constexpr { return RB + (slot == 0 ? RH : 0); };
   // Wait until raw slot s (and its header) is in, pinning its registers.
-  auto wait_raw = [&](auto SLOT, auto N) {
-    constexpr int slot = decltype(SLOT)::value, n = decltype(N)::value;
+  auto wait_raw = [&](auto SLOT, auto NW) {
+    constexpr int slot = decltype(SLOT)::value, n = decltype(NW)::value;
     static_assert(n < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
     raw[slot][0].pin_all();
@@ -468,8 +265,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     }
   };
 
-  // B fragments of the current step, [j][kk]; slot kk is replaced by the next step's
-  // word kk right after the MFMAs of slice kk have been issued.
+  // B fragments of the current step, [j][kk]; word kk is replaced by the next step's
+  // right after the MFMAs of slice kk have been issued.
   uint4 bf[2][4];
   auto decode_step = [&](auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;  // == step % 4 == sub-block quarter
@@ -478,28 +275,20 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
       for (int j = 0; j < 2; ++j) decode_hdr<QT>(hdr[j], h, sc[j]);
     }
   };
-  auto dequant_piece = [&](auto SLOT, auto KK, auto J) {
-    constexpr int slot = decltype(SLOT)::value, kk = decltype(KK)::value, j = decltype(J)::value;
-    bf[j][kk] = dequant_word<QT, XT, kk>(raw[slot][j], sc[j], slot, p.nib);
-  };
-  auto dequant_slice = [&](auto SLOT, auto KK) {
-    dequant_piece(SLOT, KK, std::integral_constant<int, 0>());
-    dequant_piece(SLOT, KK, std::integral_constant<int, 1>());
-  };
 
-  f32x16_t acc[8][2];
+  f32x16_t acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  // A fragment f = 8kk + i of a step: rows 32i + lane%32, K chunk 4h + kk, at its
-  // swizzled position.  Fragments stream through a ring of four registers, three ahead.
+  // A fragment f = MI*kk + i of a step: rows 32i + lane%32, K chunk 4h + kk, at its
+  // swizzled position.
   const int fr = lane & 31;
   auto read_a = [&](int stage, int f) -> uint4 {
-    const int kk = f >> 3, i = f & 7;
+    const int kk = f / MI, i = f % MI;
     const int r = 32 * i + fr;
     const int c = (4 * h + kk) ^ (r & 7);
     return *(const uint4*)(lds + stage * A_STAGE + r * 128 + c * 16);
@@ -518,14 +307,15 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   issue_raw(2, I2());
   issue_a(2);
   issue_raw(3, I3());
-  wait_raw(I0(), std::integral_constant<int, 24 + rops(1) + rops(2) + rops(3)>());
-  decode_step(std::integral_constant<int, 0>());
-  dequant_slice(std::integral_constant<int, 0>(), std::integral_constant<int, 0>());
-  dequant_slice(std::integral_constant<int, 0>(), std::integral_constant<int, 1>());
-  dequant_slice(std::integral_constant<int, 0>(), std::integral_constant<int, 2>());
-  dequant_slice(std::integral_constant<int, 0>(), std::integral_constant<int, 3>());
+  wait_raw(I0(), std::integral_constant<int, 3 * MI + rops(1) + rops(2) + rops(3)>());
+  decode_step(I0());
+  sfor<4>([&](auto KK) {
+    constexpr int kk = decltype(KK)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bf[j][kk] = dequant_word<QT, XT, kk>(raw[0][j], sc[j], 0, p.nib);
+  });
   // stage 0 complete (every wavefront's DMA of it) before its first fragments are read
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + rops(1) + rops(2) + rops(3)) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * MI + rops(1) + rops(2) + rops(3)) : "memory");
   __syncthreads();
   // Activation fragments stream through a ring of four registers, three ahead, across
   // step boundaries.
@@ -534,50 +324,52 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   ring[1] = read_a(0, 1);
   ring[2] = read_a(0, 2);
 
-  // Step kt (u = kt % 4), activations from LDS stage u.  64 MFMA slots, slot m = 2f + j
-  // (fragment f = 8kk + i, weight column block j); program order is issue order
+  // Step kt (u = kt % 4), activations from LDS stage u.  NSLOT MFMA slots, slot m =
+  // 2f + j (fragment f = MI*kk + i, weight column block j); program order is issue order
   // (sched_barrier fences).  Per slot: fragment f+3's LDS read (from the next step's
-  // stage past f = 28), the MFMA, and at most one small VALU task for step kt+1: in slice
-  // kk, slot t = m % 16 does the prelude (t = 0 / 8) or a quarter (t = 1..4 / 9..12) of
-  // word kk of weight row 0 / 1; the finished words replace bf[.][kk] after the slice's
-  // last MFMA.  Half way (slot 32) the wavefront waits for its DMA of stage kt+1 and
-  // joins the barrier: then stage kt+1 is complete and stage kt-1 free, so the DMA of
-  // step kt+3 goes into it.  The raw weights of step kt+4 are loaded at the end, into the
-  // ring slot step kt just used.
+  // stage near the end), the MFMA, and a share of step kt+1's dequant: per slice kk ten
+  // tasks (prelude and four quarters of word kk for weight rows 0 and 1) spread over
+  // the slice's SPS slots; the finished words replace bf[.][kk] after the slice's last
+  // MFMA.  Half way the wavefront waits for its DMA of stage kt+1 and joins the
+  // barrier: then stage kt+1 is complete and stage kt-1 free, so the DMA of step kt+3
+  // goes into it.  The raw weights of step kt+4 are loaded at the end, into the ring
+  // slot step kt just used.
   auto step = [&](int kt, auto U) {
     constexpr int u = decltype(U)::value;
     constexpr int un = (u + 1) & 3;
     using SN = std::integral_constant<int, un>;
     WordTmp<QT> wt[2];
     uint32_t nw[2][4];
-    sfor<64>([&](auto MS) {
-      constexpr int m = decltype(MS)::value, f = m >> 1, j = m & 1, kk = f >> 3, i = f & 7, t = m & 15;
-      using KK = std::integral_constant<int, kk>;
-      if constexpr (j == 0 && f + 3 < 32) ring[(f + 3) & 3] = read_a(u, f + 3);
-      if constexpr (j == 0 && f + 3 >= 32) ring[(f + 3) & 3] = read_a(un, f + 3 - 32);
+    sfor<NSLOT>([&](auto MS) {
+      constexpr int m = decltype(MS)::value, f = m >> 1, j = m & 1, kk = f / MI, i = f % MI;
+      constexpr int ts = m - kk * SPS;  // slot within the slice
+      if constexpr (j == 0 && f + 3 < NF) ring[(f + 3) & 3] = read_a(u, f + 3);
+      if constexpr (j == 0 && f + 3 >= NF) ring[(f + 3) & 3] = read_a(un, f + 3 - NF);
       acc[i][j] = mfma<XT>(bf[j][kk], ring[f & 3], acc[i][j]);
       if constexpr (m == 0) {
         // raw slot un was loaded at the end of step kt-3; since then: two steps of DMA +
         // raw loads
-        wait_raw(SN(), std::integral_constant<int, 16 + rops((u + 2) & 3) + rops((u + 3) & 3)>());
+        wait_raw(SN(), std::integral_constant<int, 2 * MI + rops((u + 2) & 3) + rops((u + 3) & 3)>());
         decode_step(SN());
       }
-      if constexpr (m == 31) {
+      if constexpr (m == NSLOT / 2 - 1) {
         // this wavefront's DMA of stage kt+1 was issued half way through step kt-2;
         // after it: the raw loads of kt+2, the DMA of stage kt+2, the raw loads of kt+3
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 + rops((u + 2) & 3) + rops((u + 3) & 3)) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(MI + rops((u + 2) & 3) + rops((u + 3) & 3)) : "memory");
         __syncthreads();
         issue_a(kt + NSTAGE - 1);
       }
-      if constexpr (t == 0 || t == 8) {
-        constexpr int jw = t >> 3;
-        word_prelude<QT, kk>(raw[un][jw], sc[jw], un, p.nib, wt[jw]);
-      }
-      if constexpr ((t >= 1 && t <= 4) || (t >= 9 && t <= 12)) {
-        constexpr int jw = t >> 3, qq = (t & 7) - 1;
-        nw[jw][qq] = word_quarter<QT, XT, kk, qq>(wt[jw], p.nib);
-      }
-      if constexpr (t == 15) {
+      // tasks k = 0..9 of the slice (0: prelude row 0, 1-4: its quarters, 5: prelude
+      // row 1, 6-9: its quarters); task k runs in slot (k * SPS) / 10
+      sfor<10>([&](auto TK_) {
+        constexpr int k = decltype(TK_)::value;
+        if constexpr ((k * SPS) / 10 == ts) {
+          constexpr int jw = k / 5, kq = k % 5;
+          if constexpr (kq == 0) word_prelude<QT, kk>(raw[un][jw], sc[jw], un, p.nib, wt[jw]);
+          else nw[jw][kq - 1] = word_quarter<QT, XT, kk, kq - 1>(wt[jw], p.nib);
+        }
+      });
+      if constexpr (ts == SPS - 1) {
         bf[0][kk] = make_uint4(nw[0][0], nw[0][1], nw[0][2], nw[0][3]);
         bf[1][kk] = make_uint4(nw[1][0], nw[1][1], nw[1][2], nw[1][3]);
       }
@@ -587,19 +379,18 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   };
 
   for (int kt = 0; kt < nkt; kt += 4) {
-    step(kt, std::integral_constant<int, 0>());
-    if (kt + 1 < nkt) step(kt + 1, std::integral_constant<int, 1>());
-    if (kt + 2 < nkt) step(kt + 2, std::integral_constant<int, 2>());
-    if (kt + 3 < nkt) step(kt + 3, std::integral_constant<int, 3>());
+    step(kt, I0());
+    if (kt + 1 < nkt) step(kt + 1, I1());
+    if (kt + 2 < nkt) step(kt + 2, I2());
+    if (kt + 3 < nkt) step(kt + 3, I3());
   }
 
   // no DMA may still be landing in LDS when the workgroup ends
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- epilogue.  The MFMAs take the weights as the first operand, so accumulator v
-  // of tile (i, j) holds Y[m][n] for m = m0 + 32i + lane%32 and n = n0 + 64w + 32j +
-  // 8(v/4) + 4(lane/32) + v%4: four consecutive columns per lane, stored as one 8-byte
-  // (16-bit types) or 16-byte (fp32) write.
+  // ---- epilogue.  Accumulator v of tile (i, j) holds Y[m][n] for m = m0 + 32i + lane%32
+  // and n = n0 + 64w + 32j + 8(v/4) + 4(lane/32) + v%4: four consecutive columns per
+  // lane, stored as one 8-byte (16-bit types) or 16-byte (fp32) write.
   const int nb = n0 + 64 * wave + 4 * (lane >> 5);
   float bv[2][4][4];
 #pragma unroll
@@ -611,14 +402,14 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
         const int n = nb + 32 * j + 8 * q + e;
         bv[j][q][e] = (p.bias && n < N) ? load_scalar(p.bias, p.bias_dtype, n) : 0.f;
       }
-  const bool vec_ok = (N & 3) == 0;
+  const bool vec_ok = (N & 3) == 0 && (p.ldy & 3) == 0;
   auto epi = [&](auto YTC) {
     constexpr int yt = decltype(YTC)::value;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < MI; ++i) {
       const int m = m0 + 32 * i + (lane & 31);
       if (m >= M) continue;
-      const size_t rowbase = (size_t)m * (size_t)N;
+      const size_t rowbase = (size_t)m * (size_t)p.ldy;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -649,51 +440,98 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   else epi(std::integral_constant<int, DT_F32>());
 }
 
-template <int QT, int XT>
+template <int QT, int XT, int MI>
 hipError_t launch_tile_t(const TileParams& tp, hipStream_t s) {
+  constexpr int lds_bytes = NSTAGE * 32 * MI * TK * 2;
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)qgemm_tile_kernel<QT, XT>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, TILE_LDS);
+    const hipError_t e = hipFuncSetAttribute((const void*)qgemm_tile_kernel<QT, XT, MI>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  qgemm_tile_kernel<QT, XT><<<dim3((unsigned)(tp.tiles_m * tp.tiles_n)), dim3(256), TILE_LDS, s>>>(tp);
+  qgemm_tile_kernel<QT, XT, MI><<<dim3((unsigned)(tp.tiles_m * tp.tiles_n)), dim3(256), lds_bytes, s>>>(tp);
   return hipGetLastError();
 }
 
-}  // namespace
-
-bool tile_fits(const RunArgs& a) {
-  for (int i = 0; i < a.L.nplanes; ++i)
-    if (a.L.size[i] >= (1u << 31)) return false;
-  return (size_t)a.M * a.L.K * 2 < (1u << 31);
+int device_cus() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      v > 0)
+    return v;
+  return 256;
 }
 
-hipError_t launch_tile(const RunArgs& a, hipStream_t s) {
-  TileParams tp;
+// 256-row tiles, unless they would leave more than a quarter of the CUs idle and
+// 128-row tiles give more of them (MLXR_MFMA_BM = 128 / 256 forces one).
+int pick_bm(int M, int N) {
+  static const int force = getenv("MLXR_MFMA_BM") ? atoi(getenv("MLXR_MFMA_BM")) : 0;
+  if (force == 128 || force == 256) return force;
+  const long tn = (N + TN - 1) / TN;
+  const long t256 = ((M + 255) / 256) * tn, t128 = ((M + 127) / 128) * tn;
+  return (4 * t256 < 3 * (long)device_cus() && t128 > t256) ? 128 : 256;
+}
+
+template <int QT, int XT>
+hipError_t launch_q(TileParams tp, hipStream_t s) {
+  const int bm = pick_bm(tp.M, tp.N);
+  tp.tiles_m = (tp.M + bm - 1) / bm;
+  tp.tiles_n = (tp.N + TN - 1) / TN;
+  return bm == 128 ? launch_tile_t<QT, XT, 4>(tp, s) : launch_tile_t<QT, XT, 8>(tp, s);
+}
+
+hipError_t launch_chunk(const TileParams& tp, int qtype, bool f16, hipStream_t s) {
+  switch (qtype) {
+    case QT_Q4_K: return f16 ? launch_q<QT_Q4_K, X_F16>(tp, s) : launch_q<QT_Q4_K, X_BF16>(tp, s);
+    case QT_Q6_K: return f16 ? launch_q<QT_Q6_K, X_F16>(tp, s) : launch_q<QT_Q6_K, X_BF16>(tp, s);
+    default: return f16 ? launch_q<QT_Q8_0, X_F16>(tp, s) : launch_q<QT_Q8_0, X_BF16>(tp, s);
+  }
+}
+
+size_t dtype_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+}  // namespace
+
+// Kernels address operands with 32-bit buffer offsets; problems whose activations or
+// weight planes reach 2 GiB run as several launches over M and N chunks (plane bytes are
+// a whole number per weight row, so an N chunk is a row range of every plane).
+hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
+  const int M = a.M, N = a.L.N, K = a.L.K;
+  // (MLXR_MFMA_CHUNK_BYTES lowers the limit, so tests can exercise the chunked launches)
+  const char* cl = getenv("MLXR_MFMA_CHUNK_BYTES");
+  const size_t lim = cl ? std::min((size_t)1 << 31, (size_t)std::max(1LL, atoll(cl))) : (size_t)1 << 31;
+  size_t prb[4] = {0, 0, 0, 0};
+  size_t max_prb = 1;
+  for (int i = 0; i < a.L.nplanes; ++i) {
+    prb[i] = a.L.size[i] / (size_t)N;
+    max_prb = std::max(max_prb, prb[i]);
+  }
+  const int Mc = (int)std::max<size_t>(256, ((lim - 1) / ((size_t)K * 2)) / 256 * 256);
+  const int Nc = (int)std::max<size_t>(TN, ((lim - 1) / max_prb) / TN * TN);
   const PlanePtrs P = plane_ptrs(a.L, a.packed);
-  for (int i = 0; i < 4; ++i) {
-    tp.P[i] = P.p[i];
-    tp.psize[i] = i < a.L.nplanes ? (uint32_t)a.L.size[i] : 0u;
+  const size_t ye = dtype_bytes(a.y_dtype), be = dtype_bytes(a.bias_dtype);
+  for (int mc = 0; mc < M; mc += Mc) {
+    for (int nc = 0; nc < N; nc += Nc) {
+      TileParams tp;
+      tp.M = std::min(Mc, M - mc);
+      tp.N = std::min(Nc, N - nc);
+      tp.K = K;
+      tp.ldy = N;
+      for (int i = 0; i < 4; ++i) {
+        tp.P[i] = P.p[i] ? P.p[i] + (size_t)nc * prb[i] : nullptr;
+        tp.psize[i] = i < a.L.nplanes ? (uint32_t)((size_t)tp.N * prb[i]) : 0u;
+      }
+      tp.x = (const uint8_t*)a.x + (size_t)mc * K * 2;
+      tp.y = (uint8_t*)a.y + ((size_t)mc * N + nc) * ye;
+      tp.bias = a.bias ? (const uint8_t*)a.bias + (size_t)nc * be : nullptr;
+      tp.bias_dtype = a.bias_dtype;
+      tp.y_dtype = a.y_dtype;
+      tp.nib = 0x0F0F0F0Fu;
+      const hipError_t e = launch_chunk(tp, a.L.qtype, a.x_dtype == DT_F16, s);
+      if (e != hipSuccess) return e;
+    }
   }
-  tp.x = a.x;
-  tp.bias = a.bias;
-  tp.y = a.y;
-  tp.M = a.M;
-  tp.N = a.L.N;
-  tp.K = a.L.K;
-  tp.bias_dtype = a.bias_dtype;
-  tp.y_dtype = a.y_dtype;
-  tp.tiles_m = (a.M + TM - 1) / TM;
-  tp.tiles_n = (a.L.N + TN - 1) / TN;
-  tp.nib = 0x0F0F0F0Fu;
-  const bool f16 = a.x_dtype == DT_F16;
-  switch (a.L.qtype) {
-    case QT_Q4_K: return f16 ? launch_tile_t<QT_Q4_K, X_F16>(tp, s) : launch_tile_t<QT_Q4_K, X_BF16>(tp, s);
-    case QT_Q6_K: return f16 ? launch_tile_t<QT_Q6_K, X_F16>(tp, s) : launch_tile_t<QT_Q6_K, X_BF16>(tp, s);
-    default: return f16 ? launch_tile_t<QT_Q8_0, X_F16>(tp, s) : launch_tile_t<QT_Q8_0, X_BF16>(tp, s);
-  }
+  return hipSuccess;
 }
 
 }  // namespace mlxr

@@ -35,8 +35,10 @@ def test_graph_replays_match_eager(cuda, M):
         layer()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
+    # capture on the stream that ran the warm-up call: the library's split-K workspace is
+    # per stream and is allocated outside capture
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         layer()
     for it in range(4):
         for y in ys.values():

@@ -193,3 +193,35 @@ def test_grouped_equals_separate_calls(cuda, M):
         ref = orc.gemm_f64(int(w.qtype), M, w.N, K, mx.synth_gguf(w.qtype, w.N, K, 200 + i), xf,
                            bias=None if biases[i] is None else biases[i].float().cpu().numpy())
         assert orc.normwise_rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("qt,M,N,K", [(Q4K, 300, 512, 4096), (Q6K, 256, 256, 2048), (Q80, 130, 384, 1056),
+                                      (Q4K, 64, 1024, 14336)])
+def test_mfma_few_tiles_long_k(cuda, qt, M, N, K):
+    """Few output tiles (the 128-row tile variant) and long K, with bias; two calls in a
+    row agree bit for bit."""
+    import torch
+    w, pw = _packed(torch, qt, N, K, 131 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 132 + N, cuda)
+    bias = torch.linspace(-2, 2, N, device=cuda).to(torch.float32)
+    y1 = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    assert torch.equal(y1, y2)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bias.cpu().numpy(), w_to_bf16=True)
+    assert orc.normwise_rel_err(y1.cpu().numpy(), ref) <= TOL
+
+
+def test_mfma_chunked_launches(cuda, monkeypatch):
+    """Operands past the 32-bit offset range run as several launches over M and N chunks;
+    a lowered chunk limit makes small shapes take that path (three M chunks, three N
+    chunks), which must stay within tolerance like the single launch."""
+    import torch
+    qt, M, N, K = Q4K, 600, 700, 1024
+    w, pw = _packed(torch, qt, N, K, 141, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 142, cuda)
+    y1 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    monkeypatch.setenv("MLXR_MFMA_CHUNK_BYTES", str(1 << 17))  # 256-row and 256-column chunks
+    y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
+    assert orc.normwise_rel_err(y2.cpu().numpy(), ref) <= TOL
+    assert orc.normwise_rel_err(y1.cpu().numpy(), ref) <= TOL
