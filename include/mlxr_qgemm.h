@@ -58,9 +58,10 @@ enum {
 
 /* Execution path selector for mlxr_qgemm_run_ex. */
 enum {
-  MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M <= 64, MFMA GEMM otherwise */
+  MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M <= 4; MFMA kernels above: skinny (weights
+                         streamed once) for M <= 64, tiled GEMM beyond */
   MLXR_PATH_GEMV = 1, /* force the wavefront-reduction GEMV kernel (any M <= 64) */
-  MLXR_PATH_MFMA = 2  /* force the bf16-MFMA GEMM (any M >= 1) */
+  MLXR_PATH_MFMA = 2  /* force the MFMA kernels (skinny for M <= 64, tiled above) */
 };
 
 /* Library version (major*10000 + minor*100 + patch). */

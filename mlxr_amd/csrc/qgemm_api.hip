@@ -15,6 +15,9 @@
 
 namespace {
 
+// Largest M the automatic path sends to the GEMV kernel.
+constexpr int kGemvMaxM = 4;
+
 thread_local std::string g_err;
 
 int fail(int code, const char* fmt, ...) {
@@ -161,8 +164,13 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
   a.y = y_dev;
   a.y_dtype = y_dtype;
   a.M = M;
-  const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= 64);
-  const hipError_t e = gemv ? mlxr::launch_gemv(a, (hipStream_t)stream) : mlxr::launch_mfma(a, (hipStream_t)stream);
+  // GEMV (no MFMA) for decode; MFMA kernels otherwise: the skinny one up to M = 64, the
+  // tiled one above (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
+  const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= kGemvMaxM);
+  hipError_t e;
+  if (gemv) e = mlxr::launch_gemv(a, (hipStream_t)stream);
+  else if (M <= 64) e = mlxr::launch_skinny(a, (hipStream_t)stream);
+  else e = mlxr::launch_mfma(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, gemv ? "gemv launch" : "mfma launch");
   return MLXR_OK;
 }

@@ -45,4 +45,7 @@ hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s
 // MFMA GEMM (qgemm_tile.hip).  Any M >= 1 (rows beyond M are masked).
 hipError_t launch_mfma(const RunArgs& a, hipStream_t s);
 
+// Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.
+hipError_t launch_skinny(const RunArgs& a, hipStream_t s);
+
 }  // namespace mlxr

@@ -1,0 +1,267 @@
+// Skinny GEMM for 4 < M <= 64 (batched decode): Y[M,N] = X[M,K] . W[N,K]^T (+ bias) on
+// 32x32x16 MFMA, streaming every weight byte from HBM exactly once.
+//
+// At these M the VALU dot products of the GEMV kernel cost M/2 operations per weight and
+// fall far behind HBM; here each weight is dequantized once in registers (the routines
+// of qgemm_wdequant.h, the ones the prefill GEMM and mlxr_qgemm_dequant use) and the M
+// rows of activations ride along in the MFMA: per 64-wide K step a lane decodes one
+// 32-weight sub-block, about three VALU operations per weight, independent of M.
+//
+// Work split: a workgroup owns a slab of 32 weight rows and has W wavefronts, wavefront
+// w taking the K steps [w*spw, (w+1)*spw).  Lane (n, h) of a wavefront owns weight row
+// n0 + n and, in each step, sub-block h; K is permuted inside the step exactly as in the
+// prefill GEMM (MFMA kk takes K positions 32h + 8kk .. +7 from both operands), so the
+// lane's dequantized word kk is its MFMA operand.  The weights are the first operand
+// (32 rows of N), the activations the second (32 rows of M, twice for M > 32), read from
+// global memory (they are small and stay in L2).  Raw weights are loaded seven steps
+// ahead, activations two, as branch-free buffer loads.  At the end the W partial tiles
+// meet in LDS and are added in wavefront order.
+#include <stdlib.h>
+
+#include <algorithm>
+#include <type_traits>
+#include <utility>
+
+#include "qgemm_device.h"
+#include "qgemm_internal.h"
+#include "qgemm_vmem.h"
+#include "qgemm_wdequant.h"
+
+namespace mlxr {
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+
+constexpr int TK = 64;
+constexpr int MAXW = 8;  // wavefronts per workgroup
+// raw weight ring (steps); loads run RING-1 steps ahead (Q8_0 sub-blocks are twice as
+// large, so a shorter ring keeps its registers in budget)
+template <int QT>
+constexpr int ring_steps() { return QT == QT_Q8_0 ? 4 : 8; }
+
+struct SkinnyParams {
+  PlanePtrs P;
+  uint32_t psize[4];  // plane sizes in bytes (< 2^31)
+  const void* x;
+  const void* bias;
+  void* y;
+  int M, N, K;
+  int bias_dtype, y_dtype;
+  int spw;  // K steps per wavefront (multiple of RING)
+  uint32_t nib;
+};
+
+// Compile-time loop: fn(integral_constant<int, i>) for i = 0 .. N-1, fully expanded.
+template <typename Fn, int... I>
+__device__ __forceinline__ void sfor_impl(Fn&& fn, std::integer_sequence<int, I...>) {
+  (fn(std::integral_constant<int, I>()), ...);
+}
+template <int N, typename Fn>
+__device__ __forceinline__ void sfor(Fn&& fn) {
+  sfor_impl(fn, std::make_integer_sequence<int, N>());
+}
+
+template <int XT>
+__device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f32x16_t& c) {
+  if constexpr (XT == X_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+}
+
+template <int QT, int XT, int MB>
+__global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p) {
+  constexpr int RING = ring_steps<QT>();
+  __shared__ float red[MAXW][MB][16][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = blockDim.x >> 6;
+  const int M = p.M, N = p.N, K = p.K;
+  const int nsub = K >> 5, nsb = K >> 8;
+  const int nkt = (K + TK - 1) / TK;
+  const int n0 = blockIdx.x * 32;
+  const int h = lane >> 5, n = n0 + (lane & 31);
+  const bool rok = n < N;
+  const uint32_t row_sub = rok ? (uint32_t)n * (uint32_t)nsub : 0u, row_sb = rok ? (uint32_t)n * (uint32_t)nsb : 0u;
+  const int kt0 = wave * p.spw, kt1 = min(nkt, kt0 + p.spw);
+  rsrc_t R[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, p.psize[i]);
+  const rsrc_t RX = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+
+  // activation rows of the second operand: mb*32 + lane%32; lane half h reads K
+  // positions 32h + 8kk .. +7 of each step (kk at immediate offset 16kk)
+  uint32_t xoff[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = mb * 32 + (lane & 31);
+    xoff[mb] = m < M ? ((uint32_t)m * (uint32_t)K + 32u * h) * 2u : OOB;
+  }
+  const int ktail = K % TK;  // Q8_0 can end on a half step
+  u32x4_t xf[4][4][MB];  // ring: step s in slot s % 4
+  auto load_x = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+    const bool live = kt < kt1 && !(ktail != 0 && kt == nkt - 1 && 32 * h >= ktail);
+    const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane(kt * TK * 2);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const uint32_t vo = live ? xoff[mb] : OOB;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) xf[slot][kk][mb] = __builtin_amdgcn_raw_buffer_load_b128(RX, vo + 16 * kk, soff, 0);
+    }
+  };
+
+  Raw<QT> raw[RING];
+  Hdr<QT> hdr[2];  // super-blocks of ring slots 0-3 and 4-7
+  Scales<QT> sc;
+  auto issue_raw = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+    const int sb = 2 * kt + h;
+    const bool in = kt < kt1 && sb < nsub && rok;
+    load_raw<QT>(R, row_sub, sb, in, raw[slot]);
+    if constexpr (QT != QT_Q8_0 && (slot & 3) == 0) load_hdr<QT>(R, row_sb, kt >> 2, in, hdr[slot >> 2]);
+  };
+
+  f32x16_t acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[mb][v] = 0.f;
+
+  // Step s issues the raw loads of step s+7 and the activations of step s+2.  The
+  // prologue issues raw loads of steps kt0 .. kt0+6 and activations of kt0, kt0+1.
+  sfor<RING - 1>([&](auto S_) {
+    constexpr int s_ = decltype(S_)::value;
+    issue_raw(kt0 + s_, std::integral_constant<int, s_>());
+  });
+  load_x(kt0, std::integral_constant<int, 0>());
+  load_x(kt0 + 1, std::integral_constant<int, 1>());
+  // step kt = kt0 + 8i + u: raw slot u, activations from xf[u % 4]
+  auto step = [&](int kt, auto U) {
+    constexpr int u = decltype(U)::value;
+    issue_raw(kt + RING - 1, std::integral_constant<int, (u + RING - 1) % RING>());
+    load_x(kt + 2, std::integral_constant<int, (u + 2) & 3>());
+    if constexpr (QT != QT_Q8_0 && (u & 3) == 0) decode_hdr<QT>(hdr[u >> 2], h, sc);
+    uint4 w[4];
+    w[0] = dequant_word<QT, XT, 0>(raw[u], sc, u & 3, p.nib);
+    w[1] = dequant_word<QT, XT, 1>(raw[u], sc, u & 3, p.nib);
+    w[2] = dequant_word<QT, XT, 2>(raw[u], sc, u & 3, p.nib);
+    w[3] = dequant_word<QT, XT, 3>(raw[u], sc, u & 3, p.nib);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const u32x4_t xv = xf[u & 3][kk][mb];
+        acc[mb] = mfma<XT>(w[kk], make_uint4(xv[0], xv[1], xv[2], xv[3]), acc[mb]);
+      }
+  };
+  // whole rings, unconditionally: steps past kt1 load nothing and add zeros, and
+  // straight-line code lets the compiler keep its load waits exact
+  for (int kt = kt0; kt < kt1; kt += RING) {
+    sfor<RING>([&](auto U_) {
+      constexpr int u = decltype(U_)::value;
+      step(kt + u, std::integral_constant<int, u>());
+    });
+  }
+
+  // partial tiles meet in LDS; thread (mb, lane) adds the nw partials of its 16
+  // accumulators in wavefront order.  Accumulator v holds Y[m][n] for m = mb*32 +
+  // lane%32, n = n0 + 8(v/4) + 4(lane/32) + v%4.
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) red[wave][mb][v][lane] = acc[mb][v];
+  __syncthreads();
+  if (tid >= 64 * MB) return;
+  const int mb = tid >> 6;
+  const int m = mb * 32 + (lane & 31);
+  if (m >= M) return;
+  float out[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    float s = 0.f;
+    for (int w = 0; w < nw; ++w) s += red[w][mb][v][lane];
+    out[v] = s;
+  }
+  const size_t rowbase = (size_t)m * N;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int nn = n0 + 8 * q + 4 * (lane >> 5);
+    float v4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v4[e] = out[4 * q + e] + ((p.bias && nn + e < N) ? load_scalar(p.bias, p.bias_dtype, nn + e) : 0.f);
+    if ((N & 3) == 0 && nn + 3 < N && p.y_dtype != DT_F32) {
+      const uint32_t lo = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[0], v4[1]) : pack2<X_F16>(v4[0], v4[1]);
+      const uint32_t hi = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[2], v4[3]) : pack2<X_F16>(v4[2], v4[3]);
+      *(uint2*)((uint16_t*)p.y + rowbase + nn) = make_uint2(lo, hi);
+    } else if ((N & 3) == 0 && nn + 3 < N) {
+      *(float4*)((float*)p.y + rowbase + nn) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nn + e < N) store_scalar(p.y, p.y_dtype, rowbase + nn + e, v4[e]);
+    }
+  }
+}
+
+int device_cus_s() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    cus = (hipGetDevice(&dev) == hipSuccess &&
+           hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+              ? v
+              : 256;
+  }
+  return cus;
+}
+
+template <int QT, int XT>
+hipError_t launch_s(SkinnyParams sp, hipStream_t s) {
+  const int slabs = (sp.N + 31) / 32;
+  const int nkt = (sp.K + TK - 1) / TK;
+  // wavefronts per slab: enough for about eight per CU, at most MAXW; each takes a whole
+  // number of rings of steps, so the ranges start on super-block boundaries
+  static const int wpc = getenv("MLXR_SKINNY_WPC") ? atoi(getenv("MLXR_SKINNY_WPC")) : 8;
+  const long want = (long)wpc * device_cus_s();
+  int w = (int)std::min<long>(MAXW, std::max<long>(1, (want + slabs - 1) / slabs));
+  constexpr int RING = ring_steps<QT>();
+  int spw = (((nkt + w - 1) / w) + RING - 1) / RING * RING;
+  w = (nkt + spw - 1) / spw;
+  sp.spw = spw;
+  const dim3 grid((unsigned)slabs), block((unsigned)(64 * w));
+  if (sp.M <= 32) qgemm_skinny_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
+  else qgemm_skinny_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_skinny(const RunArgs& a, hipStream_t s) {
+  SkinnyParams sp;
+  sp.P = plane_ptrs(a.L, a.packed);
+  for (int i = 0; i < 4; ++i) sp.psize[i] = i < a.L.nplanes ? (uint32_t)a.L.size[i] : 0u;
+  sp.x = a.x;
+  sp.bias = a.bias;
+  sp.y = a.y;
+  sp.M = a.M;
+  sp.N = a.L.N;
+  sp.K = a.L.K;
+  sp.bias_dtype = a.bias_dtype;
+  sp.y_dtype = a.y_dtype;
+  sp.nib = 0x0F0F0F0Fu;
+  const bool f16 = a.x_dtype == DT_F16;
+  switch (a.L.qtype) {
+    case QT_Q4_K: return f16 ? launch_s<QT_Q4_K, X_F16>(sp, s) : launch_s<QT_Q4_K, X_BF16>(sp, s);
+    case QT_Q6_K: return f16 ? launch_s<QT_Q6_K, X_F16>(sp, s) : launch_s<QT_Q6_K, X_BF16>(sp, s);
+    default: return f16 ? launch_s<QT_Q8_0, X_F16>(sp, s) : launch_s<QT_Q8_0, X_BF16>(sp, s);
+  }
+}
+
+}  // namespace mlxr

@@ -13,9 +13,10 @@
 //    (no VGPR staging), four stages, three steps ahead.  A BM x 64 stage has 128-byte
 //    rows; the 16-byte chunk c of row r is stored at position c ^ (r & 7), so the
 //    fragment reads of eight consecutive rows hit eight different 16-byte bank groups.
-//    The DMA and the weight loads are issued from inline assembly, so the compiler
-//    (which would otherwise wait for every outstanding load before each LDS read) leaves
-//    all memory waits to the exact vmcnt values computed from the fixed issue order.
+//    The DMA is issued from inline assembly, so the compiler (which would otherwise wait
+//    for every outstanding load before each LDS read) leaves the stage waits to the
+//    exact vmcnt values computed from the fixed issue order; the weight loads are
+//    ordinary buffer loads the compiler waits for itself.
 //  * Weights never pass through LDS.  K is permuted inside each 64-step so that in MFMA
 //    kk (0..3) lane half h supplies K positions 32h + 8kk .. +7 for both operands: lane
 //    (n, h) then owns exactly sub-block h of the step for its weight rows n and n + 32,
@@ -39,6 +40,7 @@
 
 #include "qgemm_device.h"
 #include "qgemm_internal.h"
+#include "qgemm_vmem.h"
 #include "qgemm_wdequant.h"
 
 namespace mlxr {
@@ -48,9 +50,7 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
-typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 
-constexpr uint32_t OOB = 0x80000000u;  // voffset beyond every buffer: loads return 0
 constexpr int TN = 256, TK = 64;
 constexpr int NSTAGE = 4;              // activation stages (DMA three steps ahead)
 constexpr int PD = 4;                  // raw weight prefetch distance (steps)
@@ -67,65 +67,6 @@ struct TileParams {
   int tiles_m, tiles_n;
   uint32_t nib;  // 0x0F0F0F0F, passed at run time (keeps the byte converts)
 };
-
-// Loads from inline assembly: the compiler neither sees nor waits for them; every wait
-// is an explicit s_waitcnt vmcnt(n) computed from the fixed issue order, followed by
-// pin() on the registers it covers (an empty asm that makes their later uses depend on
-// the wait).  Rows and sub-blocks past the end use an out-of-range offset and read 0.
-__device__ __forceinline__ u32x4_t vload16(const i32x4_t& r, uint32_t voff) {
-  u32x4_t v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=&v"(v) : "v"(voff), "s"(r));
-  return v;
-}
-__device__ __forceinline__ u32x4_t vload16_o16(const i32x4_t& r, uint32_t voff) {
-  u32x4_t v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:16" : "=&v"(v) : "v"(voff), "s"(r));
-  return v;
-}
-__device__ __forceinline__ u32x2_t vload8(const i32x4_t& r, uint32_t voff) {
-  u32x2_t v;
-  asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen" : "=&v"(v) : "v"(voff), "s"(r));
-  return v;
-}
-__device__ __forceinline__ uint32_t vload_u16(const i32x4_t& r, uint32_t voff) {
-  uint32_t v;
-  asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=&v"(v) : "v"(voff), "s"(r));
-  return v;
-}
-// VMEM instructions of one step's raw loads (two weight rows), and of its header loads.
-template <int QT>
-constexpr int raw_loads() { return QT == QT_Q4_K ? 2 : QT == QT_Q6_K ? 4 : 6; }
-template <int QT>
-constexpr int hdr_loads() { return QT == QT_Q4_K ? 2 : QT == QT_Q6_K ? 4 : 0; }
-
-template <int QT>
-__device__ __forceinline__ void load_raw(const i32x4_t* R, uint32_t row_sub, int sb, bool ok, Raw<QT>& r) {
-  // row_sub = row * nsub (sub-block index of the row start); sb = sub-block within the row
-  const uint32_t s = row_sub + (uint32_t)sb;
-  if constexpr (QT == QT_Q4_K) {
-    r.q = vload16(R[0], ok ? s * 16u : OOB);
-  } else if constexpr (QT == QT_Q6_K) {
-    r.ql = vload16(R[0], ok ? s * 16u : OOB);
-    r.qh = vload8(R[1], ok ? s * 8u : OOB);
-  } else {
-    const uint32_t o = ok ? s * 32u : OOB;
-    r.a = vload16(R[0], o);
-    r.b = vload16_o16(R[0], o);
-    r.d = vload_u16(R[1], ok ? s * 2u : OOB);
-  }
-}
-
-template <int QT>
-__device__ __forceinline__ void load_hdr(const i32x4_t* R, uint32_t row_sb, int g, bool ok, Hdr<QT>& h) {
-  // row_sb = row * nsb; g = super-block within the row
-  const uint32_t s = row_sb + (uint32_t)g;
-  if constexpr (QT == QT_Q4_K) {
-    h.h = vload16(R[1], ok ? s * 16u : OOB);
-  } else if constexpr (QT == QT_Q6_K) {
-    h.h = vload16(R[2], ok ? s * 16u : OOB);
-    h.d = vload_u16(R[3], ok ? s * 2u : OOB);
-  }
-}
 
 template <int XT>
 __device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f32x16_t& c) {
@@ -170,18 +111,9 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK - 1) / TK;
 
-  auto srsrc = [](const void* ptr, uint32_t bytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)ptr;
-    i32x4_t r;
-    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-    r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
-    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
-    r[3] = 0x00020000;
-    return r;
-  };
-  i32x4_t R[4];
+  rsrc_t R[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) R[i] = srsrc(p.P[i] ? p.P[i] : (const uint8_t*)p.x, p.psize[i]);
+  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P[i] ? p.P[i] : (const uint8_t*)p.x, p.psize[i]);
 
   // --- activations: LDS DMA.  Wave w fills slot blocks MI*w .. MI*w+MI-1 of a stage
   // (1 KiB = 8 rows each); lane l of block b brings row 8b + l/8, global chunk
@@ -195,7 +127,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   }
   const int ktail = K % TK;  // only Q8_0 can end on a half step (32 of 64)
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
-  const i32x4_t rx = srsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+  const i32x4_t rx = make_srsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
   // Always MI DMA instructions per wavefront and step (steps past the end read zeros
   // into a stage nobody reads), so the wait counts below are exact.
   auto issue_a = [&](int kt) {
@@ -250,21 +182,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   };
 
   // VMEM instructions issue_raw issues for the step with ring slot s.
-  constexpr int RB = raw_loads<QT>(), RH = hdr_loads<QT>();
+  constexpr int RB = 2 * raw_loads<QT>(), RH = 2 * hdr_loads<QT>();  // two weight rows
   auto rops = [](int slot) constexpr { return RB + (slot == 0 ? RH : 0); };
-  // Wait until raw slot s (and its header) is in, pinning its registers.
-  auto wait_raw = [&](auto SLOT, auto NW) {
-    constexpr int slot = decltype(SLOT)::value, n = decltype(NW)::value;
-    static_assert(n < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-    raw[slot][0].pin_all();
-    raw[slot][1].pin_all();
-    if constexpr (QT != QT_Q8_0 && slot == 0) {
-      hdr[0].pin_all();
-      hdr[1].pin_all();
-    }
-  };
-
   // B fragments of the current step, [j][kk]; word kk is replaced by the next step's
   // right after the MFMAs of slice kk have been issued.
   uint4 bf[2][4];
@@ -307,7 +226,6 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   issue_raw(2, I2());
   issue_a(2);
   issue_raw(3, I3());
-  wait_raw(I0(), std::integral_constant<int, 3 * MI + rops(1) + rops(2) + rops(3)>());
   decode_step(I0());
   sfor<4>([&](auto KK) {
     constexpr int kk = decltype(KK)::value;
@@ -315,7 +233,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     for (int j = 0; j < 2; ++j) bf[j][kk] = dequant_word<QT, XT, kk>(raw[0][j], sc[j], 0, p.nib);
   });
   // stage 0 complete (every wavefront's DMA of it) before its first fragments are read
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * MI + rops(1) + rops(2) + rops(3)) : "memory");
+  vm_wait<2 * MI + rops(1) + rops(2) + rops(3)>();
   __syncthreads();
   // Activation fragments stream through a ring of four registers, three ahead, across
   // step boundaries.
@@ -346,16 +264,11 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
       if constexpr (j == 0 && f + 3 < NF) ring[(f + 3) & 3] = read_a(u, f + 3);
       if constexpr (j == 0 && f + 3 >= NF) ring[(f + 3) & 3] = read_a(un, f + 3 - NF);
       acc[i][j] = mfma<XT>(bf[j][kk], ring[f & 3], acc[i][j]);
-      if constexpr (m == 0) {
-        // raw slot un was loaded at the end of step kt-3; since then: two steps of DMA +
-        // raw loads
-        wait_raw(SN(), std::integral_constant<int, 2 * MI + rops((u + 2) & 3) + rops((u + 3) & 3)>());
-        decode_step(SN());
-      }
+      if constexpr (m == 0) decode_step(SN());
       if constexpr (m == NSLOT / 2 - 1) {
         // this wavefront's DMA of stage kt+1 was issued half way through step kt-2;
         // after it: the raw loads of kt+2, the DMA of stage kt+2, the raw loads of kt+3
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(MI + rops((u + 2) & 3) + rops((u + 3) & 3)) : "memory");
+        vm_wait<MI + rops((u + 2) & 3) + rops((u + 3) & 3)>();
         __syncthreads();
         issue_a(kt + NSTAGE - 1);
       }
@@ -386,7 +299,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   }
 
   // no DMA may still be landing in LDS when the workgroup ends
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  vm_wait<0>();
 
   // ---- epilogue.  Accumulator v of tile (i, j) holds Y[m][n] for m = m0 + 32i + lane%32
   // and n = n0 + 64w + 32j + 8(v/4) + 4(lane/32) + v%4: four consecutive columns per
