@@ -12,6 +12,8 @@ drop-in step (one q_gemm_dequant per projection) is reported beside it.
 The other BASELINE configurations are reported under "configs":
   c1  Q8_0 GEMV, TinyLlama-1.1B q_proj (M=1, K=N=2048, fp16)
   c3  Q4_K skinny GEMM, gate/up/down, M in {8,16,32,64} (GEMV kernel and MFMA kernel)
+(c1, c3 and c4 time each call inside a replayed hipGraph of back-to-back calls, so host
+launch overhead is not in their figures.)
   c4  Q4_K prefill GEMM, Llama-3-8B set, M in {512, 2048} (bf16 MFMA)
   c5  Llama-3-70B layer, Q4_K + Q6_K (v, down), 7 GEMMs in a hipGraph at M=1 and M=256
 The CPU baseline is the reference's CPU path (dequantize all of W to fp32, then the naive
@@ -78,6 +80,21 @@ class Ctx:
         b.record(self.stream)
         torch.cuda.synchronize()
         return a.elapsed_time(b) / reps
+
+    def graph_ms(self, fn, n, replays=5):
+        """Per-call time of fn(0..n-1) captured into one graph and replayed (no host launch
+        overhead in the figure)."""
+        torch = self.torch
+        g = self.graph(lambda: [fn(r) for r in range(n)])
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(self.stream)
+        for _ in range(replays):
+            g.replay()
+        b.record(self.stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / (replays * n)
 
     def graph(self, fn):
         """Capture fn() (library launches on the capture stream) into a CUDA/HIP graph."""
@@ -241,7 +258,7 @@ def run_c1(cx, args):
     fn = lambda r: mx.q_gemm_dequant(x, copies[r % len(copies)]["q"], 1, N, K, Q80, out=y, path=mx.PATH_GEMV)
     for r in range(args.warmup):
         fn(r)
-    us = 1e3 * cx.event_ms(fn, max(args.steps, 50))
+    us = 1e3 * cx.graph_ms(fn, len(copies))
     b = gemm_bytes(mx, Q80, 1, N, K)
     return {"shape": "M=1 K=2048 N=2048 Q8_0, x/y fp16", "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
             "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": b}
@@ -261,7 +278,7 @@ def run_c3(cx, args):
             for path, pname in ((mx.PATH_GEMV, "gemv"), (mx.PATH_MFMA, "mfma")):
                 fn = lambda r: mx.q_gemm_dequant(x[K], copies[r % len(copies)][n], M, N, K, Q4K, out=y, path=path)
                 fn(0)
-                us = 1e3 * cx.event_ms(fn, max(args.steps // 2, 10))
+                us = 1e3 * cx.graph_ms(fn, 2 * len(copies))
                 row[f"{n}_{pname}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
                                        "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         res[f"M={M}"] = row
@@ -282,7 +299,7 @@ def run_c4(cx, args):
             y = torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev)
             fn = lambda r: mx.q_gemm_dequant(x[K], W[n], M, N, K, Q4K, out=y, path=mx.PATH_MFMA)
             fn(0)
-            us = 1e3 * cx.event_ms(fn, 5 if M == 2048 else 10)
+            us = 1e3 * cx.graph_ms(fn, 5 if M == 2048 else 10)
             f = 2.0 * M * N * K
             shapes[n] = {"us": round(us, 1), "TFLOPs": round(f / us / 1e6, 1)}
             tot_f += f

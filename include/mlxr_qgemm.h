@@ -118,6 +118,23 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
                       const void* x_dev, int x_dtype, const void* bias_dev, int bias_dtype,
                       void* y_dev, int y_dtype, int M, int path, void* stream);
 
+/* Device workspace bytes mlxr_qgemm_run_ws can use for an [M, N, K] problem; 0 when the
+ * problem would not use one.  MFMA GEMMs (M > 64) whose output tiles are too few to fill
+ * the device split K over several workgroups and add the fp32 partials in a second
+ * kernel; the workspace holds those partials (splits x M x N x 4 bytes).  No counterpart
+ * in the reference (its kernel has no K split, q_gemm_dequant.metal:374-464). */
+int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes);
+
+/* mlxr_qgemm_run_ex with a caller-owned device workspace (workspace_bytes bytes; NULL or
+ * too small = no K split, the result of mlxr_qgemm_run_ex).  The workspace must not be
+ * in use by other work while this call's kernels run on `stream`.  Split and unsplit
+ * results differ only in fp32 summation order; a given (shape, workspace size) always
+ * takes the same choice, so repeated calls are bit-identical. */
+int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packed_dev,
+                      const void* x_dev, int x_dtype, const void* bias_dev, int bias_dtype,
+                      void* y_dev, int y_dtype, int M, int path, void* workspace_dev,
+                      size_t workspace_bytes, void* stream);
+
 /* One weight of a grouped call (see mlxr_qgemm_run_grouped). */
 typedef struct mlxr_qgemm_item {
   int qtype, N, K, group_size; /* as in mlxr_qgemm_run */

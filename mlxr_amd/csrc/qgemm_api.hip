@@ -137,9 +137,26 @@ int mlxr_qgemm_dequant(int qtype, int N, int K, const void* packed_dev, void* ou
   return MLXR_OK;
 }
 
+int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes) {
+  mlxr::PackedLayout L;
+  const int rc = check_type_shape(qtype, N, K, &L);
+  if (rc) return rc;
+  if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
+  if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
+  *bytes = M > 64 ? mlxr::mfma_workspace_bytes(M, N, K) : 0;
+  return MLXR_OK;
+}
+
 int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packed_dev, const void* x_dev,
                       int x_dtype, const void* bias_dev, int bias_dtype, void* y_dev, int y_dtype, int M,
                       int path, void* stream) {
+  return mlxr_qgemm_run_ws(qtype, N, K, group_size, packed_dev, x_dev, x_dtype, bias_dev, bias_dtype, y_dev, y_dtype,
+                           M, path, nullptr, 0, stream);
+}
+
+int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packed_dev, const void* x_dev,
+                      int x_dtype, const void* bias_dev, int bias_dtype, void* y_dev, int y_dtype, int M,
+                      int path, void* workspace_dev, size_t workspace_bytes, void* stream) {
   mlxr::RunArgs a;
   int rc = check_type_shape(qtype, N, K, &a.L);
   if (rc) return rc;
@@ -164,6 +181,8 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
   a.y = y_dev;
   a.y_dtype = y_dtype;
   a.M = M;
+  a.ws = workspace_dev;
+  a.ws_bytes = workspace_dev ? workspace_bytes : 0;
   // GEMV (no MFMA) for decode; MFMA kernels otherwise: the skinny one up to M = 64, the
   // tiled one above (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
   const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= kGemvMaxM);

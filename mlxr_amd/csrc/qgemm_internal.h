@@ -27,6 +27,8 @@ struct RunArgs {
   void* y;
   int y_dtype;
   int M;
+  void* ws = nullptr;    // caller's device workspace for split-K partials (may be null)
+  size_t ws_bytes = 0;
 };
 
 hipError_t launch_pack(const PackedLayout& L, const uint8_t* gguf_dev, uint8_t* packed_dev,
@@ -42,8 +44,11 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s);
 bool gemv_groupable(const RunArgs& a);
 hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s);
 
-// MFMA GEMM (qgemm_tile.hip).  Any M >= 1 (rows beyond M are masked).
+// MFMA GEMM (qgemm_tile.hip).  Any M >= 1 (rows beyond M are masked).  With a.ws, shapes
+// with too few tiles for the device split K over workgroups (fp32 partials in a.ws).
 hipError_t launch_mfma(const RunArgs& a, hipStream_t s);
+// Workspace bytes launch_mfma would use for an [M, N, K] problem (0: no split).
+size_t mfma_workspace_bytes(int M, int N, int K);
 
 // Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.
 hipError_t launch_skinny(const RunArgs& a, hipStream_t s);

@@ -65,6 +65,9 @@ struct TileParams {
   int ldy;  // row stride of y in elements
   int bias_dtype, y_dtype;
   int tiles_m, tiles_n;
+  int kps;          // K steps per split (multiple of 4); the grid is tiles x splits
+  float* ws;        // split-K: fp32 partials, split s at ws + s * ws_split (row stride ldy)
+  size_t ws_split;  // elements per split plane
   uint32_t nib;  // 0x0F0F0F0F, passed at run time (keeps the byte converts)
 };
 
@@ -102,7 +105,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   // Tile order: each XCD (workgroup id % 8) takes a contiguous run of tiles in M-major
   // order, so the activation panel it walks N with stays in its L2.
   const int ntiles = p.tiles_m * p.tiles_n;
-  const int b = blockIdx.x;
+  const int split = blockIdx.x / ntiles;
+  const int b = blockIdx.x - split * ntiles;
   int t = b;
   if ((ntiles & 7) == 0) t = (b & 7) * (ntiles >> 3) + (b >> 3);
   const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
@@ -110,6 +114,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   const int M = p.M, N = p.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK - 1) / TK;
+  // this workgroup's K steps [kt0, kend): kt0 is a multiple of four (super-block start)
+  const int kt0 = split * p.kps, kend = min(nkt, kt0 + p.kps);
 
   rsrc_t R[4];
 #pragma unroll
@@ -131,7 +137,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   // Always MI DMA instructions per wavefront and step (steps past the end read zeros
   // into a stage nobody reads), so the wait counts below are exact.
   auto issue_a = [&](int kt) {
-    const bool live = kt < nkt;
+    const bool live = kt < kend;
     const bool cut = ktail != 0 && kt == nkt - 1 && a_c * 8 >= ktail;
     const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane(kt * (TK * 2));
     const uint32_t dst = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * A_STAGE + wave * MI * 1024);
@@ -171,7 +177,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   auto issue_raw = [&](int kt, auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;
     const int sb = 2 * kt + h;
-    const bool in = kt < nkt && sb < nsub;
+    const bool in = kt < kend && sb < nsub;
 #pragma unroll
     for (int j = 0; j < 2; ++j) load_raw<QT>(R, row_sub[j], sb, in && rok[j], raw[slot][j]);
     if constexpr (QT != QT_Q8_0 && slot == 0) {
@@ -219,13 +225,13 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  issue_raw(0, I0());
-  issue_a(0);
-  issue_raw(1, I1());
-  issue_a(1);
-  issue_raw(2, I2());
-  issue_a(2);
-  issue_raw(3, I3());
+  issue_raw(kt0, I0());
+  issue_a(kt0);
+  issue_raw(kt0 + 1, I1());
+  issue_a(kt0 + 1);
+  issue_raw(kt0 + 2, I2());
+  issue_a(kt0 + 2);
+  issue_raw(kt0 + 3, I3());
   decode_step(I0());
   sfor<4>([&](auto KK) {
     constexpr int kk = decltype(KK)::value;
@@ -291,70 +297,71 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     issue_raw(kt + PD, U);
   };
 
-  for (int kt = 0; kt < nkt; kt += 4) {
+  for (int kt = kt0; kt < kend; kt += 4) {
     step(kt, I0());
-    if (kt + 1 < nkt) step(kt + 1, I1());
-    if (kt + 2 < nkt) step(kt + 2, I2());
-    if (kt + 3 < nkt) step(kt + 3, I3());
+    if (kt + 1 < kend) step(kt + 1, I1());
+    if (kt + 2 < kend) step(kt + 2, I2());
+    if (kt + 3 < kend) step(kt + 3, I3());
   }
 
   // no DMA may still be landing in LDS when the workgroup ends
   vm_wait<0>();
 
-  // ---- epilogue.  Accumulator v of tile (i, j) holds Y[m][n] for m = m0 + 32i + lane%32
-  // and n = n0 + 64w + 32j + 8(v/4) + 4(lane/32) + v%4: four consecutive columns per
-  // lane, stored as one 8-byte (16-bit types) or 16-byte (fp32) write.
-  const int nb = n0 + 64 * wave + 4 * (lane >> 5);
-  float bv[2][4][4];
+  // ---- epilogue, through LDS (the activation stages are free once every wavefront is
+  // past its last fragment read).  Accumulator v of tile (i, j) holds Y[m][n] for
+  // m = m0 + 32i + lane%32, n = n0 + 64w + 32j + 8(v/4) + 4(lane/32) + v%4.  Per i, a
+  // wavefront parks its 32 x 64 block in its own LDS area (row stride 68 floats) and
+  // reads it back row-major: lane l takes columns 4(l%16) .. +3 of rows l/16 + 4r
+  // (r = 0..7), so sixteen lanes cover 64 contiguous columns of one row and every store
+  // is a whole row segment.  Split-K partials go to the workspace as fp32 without bias.
+  __syncthreads();
+  constexpr int EP_LD = 68;
+  float* ep = (float*)lds + wave * (32 * EP_LD);
+  const int c4 = lane & 15;
+  const int ncol = n0 + 64 * wave + 4 * c4;  // first of this lane's four columns
+  const bool vec_ok = (N & 3) == 0 && (p.ldy & 3) == 0 && ncol + 3 < N;
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (!p.ws && p.bias) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int e = 0; e < 4; ++e) bv[e] = ncol + e < N ? load_scalar(p.bias, p.bias_dtype, ncol + e) : 0.f;
+  }
+  void* const out = p.ws ? (void*)(p.ws + (size_t)split * p.ws_split) : p.y;
+  const int yt = p.ws ? DT_F32 : p.y_dtype;
+  sfor<MI>([&](auto I_) {
+    constexpr int i = decltype(I_)::value;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int n = nb + 32 * j + 8 * q + e;
-        bv[j][q][e] = (p.bias && n < N) ? load_scalar(p.bias, p.bias_dtype, n) : 0.f;
-      }
-  const bool vec_ok = (N & 3) == 0 && (p.ldy & 3) == 0;
-  auto epi = [&](auto YTC) {
-    constexpr int yt = decltype(YTC)::value;
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int m = m0 + 32 * i + (lane & 31);
-      if (m >= M) continue;
-      const size_t rowbase = (size_t)m * (size_t)p.ldy;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = nb + 32 * j + 8 * q;
-          const float v0 = acc[i][j][4 * q + 0] + bv[j][q][0], v1 = acc[i][j][4 * q + 1] + bv[j][q][1];
-          const float v2 = acc[i][j][4 * q + 2] + bv[j][q][2], v3 = acc[i][j][4 * q + 3] + bv[j][q][3];
-          if (vec_ok && n + 3 < N) {
-            if constexpr (yt == DT_F32) {
-              *(float4*)((float*)p.y + rowbase + n) = make_float4(v0, v1, v2, v3);
-            } else if constexpr (yt == DT_BF16) {
-              *(uint2*)((uint16_t*)p.y + rowbase + n) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
-            } else {
-              *(uint2*)((uint16_t*)p.y + rowbase + n) = make_uint2(pack2<X_F16>(v0, v1), pack2<X_F16>(v2, v3));
-            }
-          } else {
-            const float vv[4] = {v0, v1, v2, v3};
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < N) store_scalar(p.y, yt, rowbase + n + e, vv[e]);
-          }
+      for (int q = 0; q < 4; ++q)
+        *(float4*)(ep + (lane & 31) * EP_LD + 32 * j + 8 * q + 4 * (lane >> 5)) =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll 1
+    for (int r = 0; r < 8; ++r) {
+      const int row = 4 * r + (lane >> 4);
+      const float4 v = *(const float4*)(ep + row * EP_LD + 4 * c4);
+      const int m = m0 + 32 * i + row;
+      if (m < M) {
+        const float o[4] = {v.x + bv[0], v.y + bv[1], v.z + bv[2], v.w + bv[3]};
+        const size_t at = (size_t)m * (size_t)p.ldy + (size_t)ncol;
+        if (vec_ok) {
+          if (yt == DT_F32) *(float4*)((float*)out + at) = make_float4(o[0], o[1], o[2], o[3]);
+          else if (yt == DT_BF16)
+            *(uint2*)((uint16_t*)out + at) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+          else *(uint2*)((uint16_t*)out + at) = make_uint2(pack2<X_F16>(o[0], o[1]), pack2<X_F16>(o[2], o[3]));
+        } else {
+#pragma unroll 1
+          for (int e = 0; e < 4; ++e)
+            if (ncol + e < N) store_scalar(out, yt, at + e, o[e]);
         }
       }
     }
-  };
-  if (p.y_dtype == DT_BF16) epi(std::integral_constant<int, DT_BF16>());
-  else if (p.y_dtype == DT_F16) epi(std::integral_constant<int, DT_F16>());
-  else epi(std::integral_constant<int, DT_F32>());
+    __builtin_amdgcn_wave_barrier();
+  });
 }
 
 template <int QT, int XT, int MI>
-hipError_t launch_tile_t(const TileParams& tp, hipStream_t s) {
+hipError_t launch_tile_t(const TileParams& tp, int nblocks, hipStream_t s) {
   constexpr int lds_bytes = NSTAGE * 32 * MI * TK * 2;
   static bool attr_set = false;
   if (!attr_set) {
@@ -363,7 +370,7 @@ hipError_t launch_tile_t(const TileParams& tp, hipStream_t s) {
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  qgemm_tile_kernel<QT, XT, MI><<<dim3((unsigned)(tp.tiles_m * tp.tiles_n)), dim3(256), lds_bytes, s>>>(tp);
+  qgemm_tile_kernel<QT, XT, MI><<<dim3((unsigned)nblocks), dim3(256), lds_bytes, s>>>(tp);
   return hipGetLastError();
 }
 
@@ -385,19 +392,78 @@ int pick_bm(int M, int N) {
   return (4 * t256 < 3 * (long)device_cus() && t128 > t256) ? 128 : 256;
 }
 
+// Split-K plan: when the tiles of [M, N] leave more than a quarter of the CUs idle, K is
+// split into S ranges of whole super-block groups (at least eight steps each) so that
+// about one workgroup per CU runs; S <= 8.
+struct SplitPlan {
+  int bm, tiles, S, kps;
+};
+SplitPlan plan_split(int M, int N, int K) {
+  SplitPlan sp;
+  sp.bm = pick_bm(M, N);
+  sp.tiles = ((M + sp.bm - 1) / sp.bm) * ((N + TN - 1) / TN);
+  const int nkt = (K + TK - 1) / TK, cus = device_cus();
+  int S = 1;
+  if (4 * sp.tiles < 3 * cus) S = std::max(1, std::min({(cus + sp.tiles - 1) / sp.tiles, 8, nkt / 8}));
+  static const int force = getenv("MLXR_MFMA_SPLIT") ? atoi(getenv("MLXR_MFMA_SPLIT")) : 0;
+  if (force >= 1) S = std::max(1, std::min(force, (nkt + 3) / 4));
+  sp.kps = (((nkt + S - 1) / S) + 3) / 4 * 4;
+  sp.S = (nkt + sp.kps - 1) / sp.kps;
+  return sp;
+}
+
 template <int QT, int XT>
-hipError_t launch_q(TileParams tp, hipStream_t s) {
+hipError_t launch_q(TileParams tp, int S, hipStream_t s) {
   const int bm = pick_bm(tp.M, tp.N);
   tp.tiles_m = (tp.M + bm - 1) / bm;
   tp.tiles_n = (tp.N + TN - 1) / TN;
-  return bm == 128 ? launch_tile_t<QT, XT, 4>(tp, s) : launch_tile_t<QT, XT, 8>(tp, s);
+  const int ntiles = tp.tiles_m * tp.tiles_n;
+  return bm == 128 ? launch_tile_t<QT, XT, 4>(tp, ntiles * S, s) : launch_tile_t<QT, XT, 8>(tp, ntiles * S, s);
 }
 
-hipError_t launch_chunk(const TileParams& tp, int qtype, bool f16, hipStream_t s) {
+// y = sum over splits (in split order) + bias, converted to y's dtype.  VEC consecutive
+// elements per thread (VEC = 4 needs N % 4 == 0).
+template <int VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, size_t split_elems, int S,
+                                                            const void* bias, int bias_dtype, void* y, int y_dtype,
+                                                            int N, size_t total) {
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (i >= total) return;
+  float v[VEC];
+  if constexpr (VEC == 4) {
+    const float4 a = *(const float4*)(ws + i);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    for (int sp = 1; sp < S; ++sp) {
+      const float4 b = *(const float4*)(ws + (size_t)sp * split_elems + i);
+      v[0] += b.x; v[1] += b.y; v[2] += b.z; v[3] += b.w;
+    }
+  } else {
+    v[0] = ws[i];
+    for (int sp = 1; sp < S; ++sp) v[0] += ws[(size_t)sp * split_elems + i];
+  }
+  const int n = (int)(i % (size_t)N);
+  if (bias) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] += load_scalar(bias, bias_dtype, n + e);
+  }
+  if constexpr (VEC == 4) {
+    if (y_dtype == DT_F32) {
+      *(float4*)((float*)y + i) = make_float4(v[0], v[1], v[2], v[3]);
+      return;
+    }
+    const uint32_t lo = y_dtype == DT_BF16 ? pack_bf16x2(v[0], v[1]) : pack2<X_F16>(v[0], v[1]);
+    const uint32_t hi = y_dtype == DT_BF16 ? pack_bf16x2(v[2], v[3]) : pack2<X_F16>(v[2], v[3]);
+    *(uint2*)((uint16_t*)y + i) = make_uint2(lo, hi);
+  } else {
+    store_scalar(y, y_dtype, i, v[0]);
+  }
+}
+
+hipError_t launch_chunk(const TileParams& tp, int S, int qtype, bool f16, hipStream_t s) {
   switch (qtype) {
-    case QT_Q4_K: return f16 ? launch_q<QT_Q4_K, X_F16>(tp, s) : launch_q<QT_Q4_K, X_BF16>(tp, s);
-    case QT_Q6_K: return f16 ? launch_q<QT_Q6_K, X_F16>(tp, s) : launch_q<QT_Q6_K, X_BF16>(tp, s);
-    default: return f16 ? launch_q<QT_Q8_0, X_F16>(tp, s) : launch_q<QT_Q8_0, X_BF16>(tp, s);
+    case QT_Q4_K: return f16 ? launch_q<QT_Q4_K, X_F16>(tp, S, s) : launch_q<QT_Q4_K, X_BF16>(tp, S, s);
+    case QT_Q6_K: return f16 ? launch_q<QT_Q6_K, X_F16>(tp, S, s) : launch_q<QT_Q6_K, X_BF16>(tp, S, s);
+    default: return f16 ? launch_q<QT_Q8_0, X_F16>(tp, S, s) : launch_q<QT_Q8_0, X_BF16>(tp, S, s);
   }
 }
 
@@ -423,6 +489,44 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   const int Nc = (int)std::max<size_t>(TN, ((lim - 1) / max_prb) / TN * TN);
   const PlanePtrs P = plane_ptrs(a.L, a.packed);
   const size_t ye = dtype_bytes(a.y_dtype), be = dtype_bytes(a.bias_dtype);
+  // split-K (single-chunk problems with a large enough workspace only)
+  SplitPlan sp{0, 0, 1, 0};
+  if (a.ws && M <= Mc && N <= Nc) {
+    sp = plan_split(M, N, K);
+    if (sp.S > 1 && (size_t)sp.S * (size_t)M * (size_t)N * 4u > a.ws_bytes) sp.S = 1;
+  }
+  if (sp.S > 1) {
+    TileParams tp;
+    tp.M = M;
+    tp.N = N;
+    tp.K = K;
+    tp.ldy = N;
+    for (int i = 0; i < 4; ++i) {
+      tp.P[i] = P.p[i];
+      tp.psize[i] = i < a.L.nplanes ? (uint32_t)a.L.size[i] : 0u;
+    }
+    tp.x = a.x;
+    tp.y = a.y;
+    tp.bias = nullptr;
+    tp.bias_dtype = a.bias_dtype;
+    tp.y_dtype = DT_F32;
+    tp.nib = 0x0F0F0F0Fu;
+    tp.kps = sp.kps;
+    tp.ws = (float*)a.ws;
+    tp.ws_split = (size_t)M * (size_t)N;
+    hipError_t e = launch_chunk(tp, sp.S, a.L.qtype, a.x_dtype == DT_F16, s);
+    if (e != hipSuccess) return e;
+    const size_t total = (size_t)M * (size_t)N;
+    if ((N & 3) == 0) {
+      const size_t threads = total / 4;
+      splitk_reduce_kernel<4><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(
+          (const float*)a.ws, tp.ws_split, sp.S, a.bias, a.bias_dtype, a.y, a.y_dtype, N, total);
+    } else {
+      splitk_reduce_kernel<1><<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
+          (const float*)a.ws, tp.ws_split, sp.S, a.bias, a.bias_dtype, a.y, a.y_dtype, N, total);
+    }
+    return hipGetLastError();
+  }
   for (int mc = 0; mc < M; mc += Mc) {
     for (int nc = 0; nc < N; nc += Nc) {
       TileParams tp;
@@ -440,11 +544,20 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
       tp.bias_dtype = a.bias_dtype;
       tp.y_dtype = a.y_dtype;
       tp.nib = 0x0F0F0F0Fu;
-      const hipError_t e = launch_chunk(tp, a.L.qtype, a.x_dtype == DT_F16, s);
+      tp.kps = (K + TK - 1) / TK;
+      tp.ws = nullptr;
+      tp.ws_split = 0;
+      const hipError_t e = launch_chunk(tp, 1, a.L.qtype, a.x_dtype == DT_F16, s);
       if (e != hipSuccess) return e;
     }
   }
   return hipSuccess;
+}
+
+size_t mfma_workspace_bytes(int M, int N, int K) {
+  if (M <= 64 || (size_t)M * (size_t)K * 2u >= ((size_t)1 << 31)) return 0;
+  const SplitPlan sp = plan_split(M, N, K);
+  return sp.S > 1 ? (size_t)sp.S * (size_t)M * (size_t)N * 4u : 0;
 }
 
 }  // namespace mlxr

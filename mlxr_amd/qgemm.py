@@ -68,6 +68,8 @@ _SIGS = {
     "mlxr_qgemm_dequant": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run_ex": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "mlxr_qgemm_workspace_size": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_size_t)]),
+    "mlxr_qgemm_run_ws": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "mlxr_qgemm_run_grouped": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
@@ -230,11 +232,25 @@ def q_gemm_dequant(input, weights, M, N, K, quant_type, group_size=0, bias=None,
         input = input.contiguous()
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype or input.dtype, device=input.device)
-    _check(lib().mlxr_qgemm_run_ex(int(quant_type), N, K, group_size, weights.data_ptr(), input.data_ptr(),
+    # split-K workspace from torch's stream-ordered caching allocator (graph-capture safe)
+    ws_bytes = workspace_size(quant_type, N, K, M) if path != PATH_GEMV else 0
+    ws = None
+    if ws_bytes:
+        with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=input.device)
+    _check(lib().mlxr_qgemm_run_ws(int(quant_type), N, K, group_size, weights.data_ptr(), input.data_ptr(),
                                    _dt_code(input.dtype), bias.data_ptr() if bias is not None else None,
                                    _dt_code(bias.dtype) if bias is not None else F32, out.data_ptr(),
-                                   _dt_code(out.dtype), M, path, _stream_ptr(stream)))
+                                   _dt_code(out.dtype), M, path, ws.data_ptr() if ws is not None else None,
+                                   ws_bytes, _stream_ptr(stream)))
     return out
+
+
+def workspace_size(qtype, N, K, M):
+    """Device workspace bytes q_gemm_dequant uses for split-K at this shape (0 = none)."""
+    out = ctypes.c_size_t(0)
+    _check(lib().mlxr_qgemm_workspace_size(int(qtype), int(N), int(K), int(M), ctypes.byref(out)))
+    return out.value
 
 
 def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=None, stream=None):

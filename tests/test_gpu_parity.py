@@ -225,3 +225,44 @@ def test_mfma_chunked_launches(cuda, monkeypatch):
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
     assert orc.normwise_rel_err(y2.cpu().numpy(), ref) <= TOL
     assert orc.normwise_rel_err(y1.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("qt,M,N,K,ydt", [(Q4K, 512, 1024, 4096, "bf16"), (Q6K, 256, 1000, 2048, "f32"),
+                                          (Q80, 130, 384, 1056, "f16"), (Q4K, 2048, 1024, 4096, "f32")])
+def test_mfma_split_k(cuda, qt, M, N, K, ydt):
+    """Split-K through the C ABI: mlxr_qgemm_run_ws with the workspace size the library
+    asks for splits K (partials + reduce kernel) and stays within tolerance of the oracle,
+    with bias, for every output dtype and N % 4 != 0; repeated calls are bit-identical, and
+    a workspace one byte too small gives exactly the unsplit mlxr_qgemm_run_ex result."""
+    import ctypes
+    import torch
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[ydt]
+    w, pw = _packed(torch, qt, N, K, 151 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 152 + N, cuda)
+    bias = torch.linspace(-1, 1, N, device=cuda).to(torch.bfloat16)
+    wsb = mx.workspace_size(qt, N, K, M)
+    assert wsb > 0 and wsb % (4 * M * N) == 0
+    ws = torch.empty(wsb, dtype=torch.uint8, device=cuda)
+    L = mx.lib()
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run(y, wsp, nbytes):
+        rc = L.mlxr_qgemm_run_ws(int(qt), N, K, 0, pw.data_ptr(), x.data_ptr(), mx.BF16, bias.data_ptr(), mx.BF16,
+                                 y.data_ptr(), {"bf16": mx.BF16, "f16": mx.F16, "f32": mx.F32}[ydt], M,
+                                 mx.PATH_MFMA, wsp, nbytes, s)
+        assert rc == 0, L.mlxr_qgemm_last_error()
+
+    ys = [torch.empty((M, N), dtype=tdt, device=cuda) for _ in range(4)]
+    run(ys[0], ws.data_ptr(), wsb)
+    run(ys[1], ws.data_ptr(), wsb)
+    run(ys[2], ws.data_ptr(), wsb - 1)
+    rc = L.mlxr_qgemm_run_ex(int(qt), N, K, 0, pw.data_ptr(), x.data_ptr(), mx.BF16, bias.data_ptr(), mx.BF16,
+                             ys[3].data_ptr(), {"bf16": mx.BF16, "f16": mx.F16, "f32": mx.F32}[ydt], M,
+                             mx.PATH_MFMA, s)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(ys[0], ys[1])
+    assert torch.equal(ys[2], ys[3])
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bias.float().cpu().numpy(), w_to_bf16=True)
+    for y in (ys[0], ys[3]):
+        assert orc.normwise_rel_err(y.float().cpu().numpy(), ref) <= TOL
