@@ -21,8 +21,9 @@
  *     exception crosses this boundary.
  *   - Thread-safe: the library has no mutable global state besides the thread-local
  *     error string.
- *   - Dequantized weights follow the GGUF block_q8_0 / block_q4_K / block_q6_K
- *     definitions exactly (fp32 results are bit-exact to those formulas).
+ *   - Dequantized weights follow the GGUF block_q4_0 / block_q4_1 / block_q8_0 /
+ *     block_q4_K / block_q6_K definitions exactly (fp32 results are bit-exact to those
+ *     formulas).
  */
 #ifndef MLXR_QGEMM_H
 #define MLXR_QGEMM_H
@@ -35,7 +36,9 @@ extern "C" {
 #endif
 
 /* Quantization types: same numeric values as mlxr::kernels::QuantType
- * (reference q_gemm_dequant_primitive.h:18-35).  Implemented: Q8_0, Q4_K, Q6_K. */
+ * (reference q_gemm_dequant_primitive.h:18-35).  Implemented: Q4_0, Q4_1, Q8_0, Q4_K, Q6_K.
+ * Q4_0/Q4_1 follow GGUF block_q4_0/block_q4_1 (byte j holds elements j and j+16); the
+ * reference's CPU routines (.mm:189-216) read them interleaved (elements 2j, 2j+1). */
 enum {
   MLXR_Q4_0 = 0, MLXR_Q4_1 = 1, MLXR_Q8_0 = 2, MLXR_Q4_K = 3, MLXR_Q6_K = 4,
   MLXR_Q5_0 = 5, MLXR_Q5_1 = 6, MLXR_Q8_1 = 7, MLXR_Q2_K = 8, MLXR_Q3_K = 9,
@@ -161,6 +164,8 @@ int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* 
  *   Q8_0: d = RNE_fp16(|N(0,1)| * 0.02/127), qs uniform in [-127, 127]
  *   Q4_K: d, dmin = RNE_fp16(|N(0,1)| * 1e-3), 12 scale bytes and 128 qs bytes uniform
  *   Q6_K: ql, qh bytes uniform, scales uniform in [-32, 31], d = RNE_fp16(|N(0,1)|*1e-3)
+ *   Q4_0: d = RNE_fp16(|N(0,1)| * 2e-3), 16 qs bytes uniform
+ *   Q4_1: d = RNE_fp16(|N(0,1)| * 2e-3), m = RNE_fp16(N(0,1) * 8e-3), 16 qs bytes uniform
  * out_host must hold mlxr_qgemm_gguf_size bytes. */
 int mlxr_synth_gguf(int qtype, int N, int K, uint64_t seed, void* out_host);
 

@@ -30,12 +30,30 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+namespace mlxr {
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+}  // namespace mlxr
+
+namespace {
+
 int hip_fail(hipError_t e, const char* where) {
   return fail(MLXR_E_HIP, "%s: HIP error %d (%s)", where, (int)e, hipGetErrorString(e));
 }
 
 bool implemented(int qtype) {
-  return qtype == MLXR_Q8_0 || qtype == MLXR_Q4_K || qtype == MLXR_Q6_K;
+  return qtype == MLXR_Q4_0 || qtype == MLXR_Q4_1 || qtype == MLXR_Q8_0 || qtype == MLXR_Q4_K || qtype == MLXR_Q6_K;
 }
 
 int check_type_shape(int qtype, int N, int K, mlxr::PackedLayout* L) {

@@ -83,6 +83,17 @@ struct RawSub<QT_Q8_0> {
   uint32_t d;
 };
 
+template <>
+struct RawSub<QT_Q4_0> {
+  uint4 q;     // 4 pair-interleaved words
+  uint32_t d;  // fp16 bits
+};
+template <>
+struct RawSub<QT_Q4_1> {
+  uint4 q;
+  uint32_t d;  // fp16 d | fp16 m << 16
+};
+
 template <int QT>
 __device__ __forceinline__ void load_raw_sub(const uint8_t* const* planes, int K, int n, int sb, RawSub<QT>& r) {
   const size_t nsub = (size_t)(K / 32);
@@ -96,6 +107,10 @@ __device__ __forceinline__ void load_raw_sub(const uint8_t* const* planes, int K
     r.qh = *(const uint2*)(planes[1] + ((size_t)n * nsub + sb) * 8);
     r.sc = *(const uint16_t*)(planes[2] + ((size_t)n * nsb + (sb >> 3)) * 16 + 2 * (sb & 7));
     r.d = *(const uint16_t*)(planes[3] + ((size_t)n * nsb + (sb >> 3)) * 2);
+  } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {  // block index == sub-block index
+    r.q = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
+    if constexpr (QT == QT_Q4_0) r.d = *(const uint16_t*)(planes[1] + ((size_t)n * nsub + sb) * 2);
+    else r.d = *(const uint32_t*)(planes[1] + ((size_t)n * nsub + sb) * 4);
   } else {  // Q8_0: block index == sub-block index
     const uint8_t* qs = planes[0] + ((size_t)n * nsub + sb) * 32;
     r.a = *(const uint4*)qs;
@@ -131,6 +146,15 @@ __device__ __forceinline__ void dequant_raw(const RawSub<QT>& r, int j, float* w
       const uint32_t lo = (lw[e >> 3] >> pi_shift(e & 7)) & 15u;
       const uint32_t hi = (hw[e >> 4] >> q6h_shift(e)) & 3u;
       w[e] = (e < 16 ? ds0 : ds1) * (float)((int)(lo | (hi << 4)) - 32);
+    }
+  } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
+    const float d = f16_bits_to_f32(r.d & 0xffffu);
+    const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const uint32_t v = (qw[e >> 3] >> pi_shift(e & 7)) & 15u;
+      if constexpr (QT == QT_Q4_0) w[e] = (float)((int)v - 8) * d;
+      else w[e] = __builtin_fmaf((float)v, d, f16_bits_to_f32(r.d >> 16));
     }
   } else {
     const float d = f16_bits_to_f32(r.d);

@@ -125,6 +125,16 @@ struct WLoad<QT_Q8_0> {
   uint4 a, b;
   uint32_t d;
 };
+template <>
+struct WLoad<QT_Q4_0> {
+  uint4 q;
+  uint32_t d;  // fp16 bits
+};
+template <>
+struct WLoad<QT_Q4_1> {
+  uint4 q;
+  uint32_t d;  // fp16 d | fp16 m << 16
+};
 
 template <bool NT>
 __device__ __forceinline__ uint4 ldw16(const uint8_t* p) {
@@ -150,6 +160,12 @@ __device__ __forceinline__ void load_w(const PlanePtrs& P, int K, int n, int sb,
     w.qh = *(const uint2*)(P.p[1] + ((size_t)n * nsub + sb) * 8);
     w.sc = *(const uint16_t*)(P.p[2] + ((size_t)n * nsb + (sb >> 3)) * 16 + 2 * (sb & 7));
     w.d = *(const uint16_t*)(P.p[3] + ((size_t)n * nsb + (sb >> 3)) * 2);
+  } else if constexpr (QT == QT_Q4_0) {
+    w.q = ldw16<NT>(P.p[0] + ((size_t)n * nsub + sb) * 16);
+    w.d = *(const uint16_t*)(P.p[1] + ((size_t)n * nsub + sb) * 2);
+  } else if constexpr (QT == QT_Q4_1) {
+    w.q = ldw16<NT>(P.p[0] + ((size_t)n * nsub + sb) * 16);
+    w.d = *(const uint32_t*)(P.p[1] + ((size_t)n * nsub + sb) * 4);
   } else {
     const uint8_t* q = P.p[0] + ((size_t)n * nsub + sb) * 32;
     w.a = ldw16<NT>(q);
@@ -167,6 +183,9 @@ __device__ __forceinline__ void zero_w(WLoad<QT>& w) {
     w.qh = make_uint2(0, 0);
     w.sc = 0;
     w.d = 0;
+  } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
+    w.q = make_uint4(0, 0, 0, 0);
+    w.d = 0;
   } else {
     w.a = make_uint4(0, 0, 0, 0);
     w.b = make_uint4(0, 0, 0, 0);
@@ -178,6 +197,7 @@ __device__ __forceinline__ void zero_w(WLoad<QT>& w) {
 struct WDec {
   uint32_t p[16];
   float s0, s1;  // Q4_K: d*sc, dmin*m.  Q6_K: d*sc(group 0), d*sc(group 1).  Q8_0: d, -
+                 // Q4_0: d, 8d.  Q4_1: d, -m  (so Q4_0/Q4_1/Q4_K share one contribution)
 };
 
 template <int QT, int XT>
@@ -197,6 +217,15 @@ __device__ __forceinline__ void decode_w(const WLoad<QT>& w, int j, WDec& o) {
     dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0x141, 0xF, 0xF, false);
     o.s0 = f16_bits_to_f32(dd & 0xffffu) * (float)(w.h & 63u);
     o.s1 = f16_bits_to_f32(dd >> 16) * (float)((w.h >> 6) & 63u);
+  } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
+    constexpr uint32_t MAGIC = (XT == X_BF16) ? 0x43004300u : 0x64006400u;
+    const uint32_t qw[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) o.p[4 * t + s] = ((qw[t] >> (4 * s)) & 0x000F000Fu) | MAGIC;
+    o.s0 = f16_bits_to_f32(w.d & 0xffffu);
+    o.s1 = QT == QT_Q4_0 ? 8.f * o.s0 : -f16_bits_to_f32(w.d >> 16);
   } else if constexpr (QT == QT_Q6_K) {
     constexpr uint32_t MAGIC = (XT == X_BF16) ? 0x43004300u : 0x64006400u;
     const uint32_t lw[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
@@ -235,7 +264,7 @@ __device__ __forceinline__ void decode_w(const WLoad<QT>& w, int j, WDec& o) {
 // Contribution of one decoded row/sub-block against one activation sub-block.
 template <int QT, int XT>
 __device__ __forceinline__ float contrib(const uint32_t* xv, const WDec& w, float X0, float X1) {
-  if constexpr (QT == QT_Q4_K) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q4_0 || QT == QT_Q4_1) {
     constexpr float OFF = (XT == X_BF16) ? 128.f : 1024.f;
     const float S = dot_range<XT, 0, 16>(xv, w.p);
     return w.s0 * (S - OFF * (X0 + X1)) - w.s1 * (X0 + X1);
@@ -374,6 +403,16 @@ struct CLoad<QT_Q8_0> {
   uint4 a, b;
   uint16_t d;
 };
+template <>
+struct CLoad<QT_Q4_0> {
+  uint4 q;
+  uint16_t d;
+};
+template <>
+struct CLoad<QT_Q4_1> {
+  uint4 q;
+  uint32_t d;
+};
 
 // (v & mask) | bits in one VALU op; the compiler otherwise emits an and plus an or.
 __device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bits) {
@@ -417,6 +456,11 @@ __device__ __forceinline__ void load_chunk(const rsrc_t* R, int row, int seg, in
     b.qh = make_uint2(h[0], h[1]);
     b.sc = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, 0);
     b.d = __builtin_amdgcn_raw_buffer_load_b16(R[3], ok ? (lane >> 3) * 2 : OOB, gbase * 2u, 0);
+  } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    b.q = make_uint4(q[0], q[1], q[2], q[3]);
+    if constexpr (QT == QT_Q4_0) b.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, sbase * 2u, 0);
+    else b.d = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? lane * 4 : OOB, sbase * 4u, 0);
   } else {
     const u32x4_t q0 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 : OOB, sbase * 32u, 0);
     const u32x4_t q1 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 + 16 : OOB, sbase * 32u, 0);
@@ -443,6 +487,15 @@ __device__ __forceinline__ void decode_chunk(const CLoad<QT>& b, int j, uint32_t
     dd |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)dd, 0x141, 0xF, 0xF, false);
     o.s0 = f16_bits_to_f32(dd & 0xffffu) * (float)(hv & 63u);
     o.s1 = f16_bits_to_f32(dd >> 16) * (float)((hv >> 6) & 63u);
+  } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
+    const uint32_t qw[4] = {b.q.x, b.q.y, b.q.z, b.q.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) o.p[4 * t + s] = and_or(qw[t] >> (4 * s), MASK, MAGIC);
+    const uint32_t dv = b.d;
+    o.s0 = f16_bits_to_f32(dv & 0xffffu);
+    o.s1 = QT == QT_Q4_0 ? 8.f * o.s0 : -f16_bits_to_f32(dv >> 16);
   } else if constexpr (QT == QT_Q6_K) {
     WLoad<QT_Q6_K> w;
     w.ql = b.ql;
@@ -790,6 +843,8 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s) {
   switch (a.L.qtype) {
     case QT_Q4_K: return f16 ? launch_x<QT_Q4_K, X_F16>(p, a, R, s) : launch_x<QT_Q4_K, X_BF16>(p, a, R, s);
     case QT_Q6_K: return f16 ? launch_x<QT_Q6_K, X_F16>(p, a, R, s) : launch_x<QT_Q6_K, X_BF16>(p, a, R, s);
+    case QT_Q4_0: return f16 ? launch_x<QT_Q4_0, X_F16>(p, a, R, s) : launch_x<QT_Q4_0, X_BF16>(p, a, R, s);
+    case QT_Q4_1: return f16 ? launch_x<QT_Q4_1, X_F16>(p, a, R, s) : launch_x<QT_Q4_1, X_BF16>(p, a, R, s);
     default: return f16 ? launch_x<QT_Q8_0, X_F16>(p, a, R, s) : launch_x<QT_Q8_0, X_BF16>(p, a, R, s);
   }
 }
@@ -802,6 +857,8 @@ hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s
   switch (a.L.qtype) {
     case QT_Q4_K: return f16 ? launch_lds<QT_Q4_K, X_F16>(items, n, s) : launch_lds<QT_Q4_K, X_BF16>(items, n, s);
     case QT_Q6_K: return f16 ? launch_lds<QT_Q6_K, X_F16>(items, n, s) : launch_lds<QT_Q6_K, X_BF16>(items, n, s);
+    case QT_Q4_0: return f16 ? launch_lds<QT_Q4_0, X_F16>(items, n, s) : launch_lds<QT_Q4_0, X_BF16>(items, n, s);
+    case QT_Q4_1: return f16 ? launch_lds<QT_Q4_1, X_F16>(items, n, s) : launch_lds<QT_Q4_1, X_BF16>(items, n, s);
     default: return f16 ? launch_lds<QT_Q8_0, X_F16>(items, n, s) : launch_lds<QT_Q8_0, X_BF16>(items, n, s);
   }
 }

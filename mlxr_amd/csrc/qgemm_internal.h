@@ -31,6 +31,9 @@ struct RunArgs {
   size_t ws_bytes = 0;
 };
 
+// Sets the calling thread's mlxr_qgemm_last_error message; returns code.
+int set_error(int code, const char* fmt, ...);
+
 hipError_t launch_pack(const PackedLayout& L, const uint8_t* gguf_dev, uint8_t* packed_dev,
                        hipStream_t s);
 hipError_t launch_dequant(const PackedLayout& L, const uint8_t* packed_dev, void* out,

@@ -1,8 +1,8 @@
 // Packed HBM layout of a quantized [N, K] weight, shared by host and device code.
 //
-// GGUF stores a weight as N rows of K/B blocks (B = 32 for Q8_0, 256 for the K-quants),
-// each block an array-of-structs record (block_q8_0 = 34 B, block_q4_K = 144 B,
-// block_q6_K = 210 B).  The packed form splits every record into planes so that a
+// GGUF stores a weight as N rows of K/B blocks (B = 32 for Q4_0/Q4_1/Q8_0, 256 for the
+// K-quants), each block an array-of-structs record (block_q4_0 = 18 B, block_q4_1 = 20 B,
+// block_q8_0 = 34 B, block_q4_K = 144 B, block_q6_K = 210 B).  The packed form splits every record into planes so that a
 // 64-lane wavefront reading one plane touches whole, contiguous 128-byte lines, and it
 // reorders nibbles inside 32-bit words so the GEMV can turn two 4-bit weights into a
 // bf16/fp16 pair with a single mask-and-or.  It holds exactly the GGUF bytes (no
@@ -26,6 +26,11 @@
 //         plane 3  d    [N][K/256][2 B]  fp16 d
 //   Q8_0  plane 0  qs   [N][K/32][32 B]  int8, natural order
 //         plane 1  d    [N][K/32][2 B]   fp16 d
+//   Q4_0  plane 0  qs   [N][K/32][16 B]  block = 4 pair-interleaved words (q 0..15), as a
+//                                        Q4_K sub-block
+//         plane 1  d    [N][K/32][2 B]   fp16 d
+//   Q4_1  plane 0  qs   [N][K/32][16 B]  as Q4_0
+//         plane 1  dm   [N][K/32][4 B]   fp16 d | fp16 m << 16
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -52,6 +57,10 @@ struct PackedLayout {
 
 MLXR_HD inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// K-quants carry a per-super-block header (scales of eight sub-blocks); the 32-weight
+// block types carry their scale with every block.
+MLXR_HD constexpr bool is_kquant(int qtype) { return qtype == QT_Q4_K || qtype == QT_Q6_K; }
+
 // Fills L; returns false if the type is not one the kernels implement or K does not
 // split into whole blocks.
 MLXR_HD inline bool make_layout(int qtype, int N, int K, PackedLayout* L) {
@@ -72,6 +81,10 @@ MLXR_HD inline bool make_layout(int qtype, int N, int K, PackedLayout* L) {
     if (K % 32) return false;
     const size_t nb = (size_t)(K / 32);
     L->nplanes = 2; L->size[0] = n * nb * 32; L->size[1] = n * nb * 2;
+  } else if (qtype == QT_Q4_0 || qtype == QT_Q4_1) {
+    if (K % 32) return false;
+    const size_t nb = (size_t)(K / 32);
+    L->nplanes = 2; L->size[0] = n * nb * 16; L->size[1] = n * nb * (qtype == QT_Q4_1 ? 4 : 2);
   } else {
     return false;
   }

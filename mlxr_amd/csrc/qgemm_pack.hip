@@ -1,7 +1,7 @@
 // One-time repack of GGUF blocks into the planar layout, and the dequant kernel.
 //
 // Reference counterparts: the block records of core/kernels/primitives/
-// q_gemm_dequant_primitive.mm:40-57 (GGUF block_q8_0 / block_q4_K / block_q6_K), the
+// q_gemm_dequant_primitive.mm:29-57 (GGUF block_q4_0 / q4_1 / q8_0 / q4_K / q6_K), the
 // upload the reference skips at daemon/server/model_loader.cpp:236-245, and the CPU
 // dequant routines at q_gemm_dequant_primitive.mm:189-225.
 #include "qgemm_device.h"
@@ -98,6 +98,29 @@ __global__ void pack_q80_kernel(const uint8_t* __restrict__ src, uint8_t* __rest
   d_out[idx * 2 + 1] = b[1];
 }
 
+// One thread per (row, block).  Source: 18-byte block_q4_0 or 20-byte block_q4_1 records;
+// GGUF element e < 16 is the low nibble of byte e, e >= 16 the high nibble of byte e - 16.
+template <int QT>
+__global__ void pack_q4_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs_out,
+                               uint8_t* __restrict__ d_out, int N, int nb) {
+  constexpr int HB = QT == QT_Q4_1 ? 4 : 2;  // header bytes (d, and m for Q4_1)
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)N * nb) return;
+  const uint8_t* b = src + idx * (HB + 16);
+  const uint8_t* q = b + HB;
+  uint32_t* o = (uint32_t*)(qs_out + idx * 16);
+  for (int t = 0; t < 4; ++t) {
+    uint32_t w = 0;
+    for (int e = 0; e < 8; ++e) {
+      const int el = 8 * t + e;
+      const uint32_t byte = rd_u8(q, el & 15);
+      w |= (el < 16 ? (byte & 15u) : (byte >> 4)) << pi_shift(e);
+    }
+    o[t] = w;
+  }
+  for (int i = 0; i < HB; ++i) d_out[idx * HB + i] = b[i];
+}
+
 // One thread per (row, 32-weight sub-block): 32 outputs.
 template <int QT>
 __global__ void dequant_kernel(PlanePtrs P, int N, int K, void* __restrict__ out, int out_dtype, uint32_t nib) {
@@ -140,6 +163,16 @@ hipError_t launch_pack(const PackedLayout& L, const uint8_t* gguf_dev, uint8_t* 
     pack_q6k_kernel<<<dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s>>>(
         gguf_dev, packed_dev + L.off[0], packed_dev + L.off[1], packed_dev + L.off[2],
         packed_dev + L.off[3], L.N, nsb);
+  } else if (L.qtype == QT_Q4_0 || L.qtype == QT_Q4_1) {
+    const int nb = L.K / 32;
+    const size_t total = (size_t)L.N * nb;
+    const dim3 grid((unsigned)((total + threads - 1) / threads));
+    if (L.qtype == QT_Q4_0)
+      pack_q4_kernel<QT_Q4_0><<<grid, dim3(threads), 0, s>>>(gguf_dev, packed_dev + L.off[0], packed_dev + L.off[1],
+                                                             L.N, nb);
+    else
+      pack_q4_kernel<QT_Q4_1><<<grid, dim3(threads), 0, s>>>(gguf_dev, packed_dev + L.off[0], packed_dev + L.off[1],
+                                                             L.N, nb);
   } else {
     const int nb = L.K / 32;
     const size_t total = (size_t)L.N * nb;
@@ -159,6 +192,10 @@ hipError_t launch_dequant(const PackedLayout& L, const uint8_t* packed_dev, void
     dequant_kernel<QT_Q4_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   else if (L.qtype == QT_Q6_K)
     dequant_kernel<QT_Q6_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
+  else if (L.qtype == QT_Q4_0)
+    dequant_kernel<QT_Q4_0><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
+  else if (L.qtype == QT_Q4_1)
+    dequant_kernel<QT_Q4_1><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   else
     dequant_kernel<QT_Q8_0><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   return hipGetLastError();

@@ -102,7 +102,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
     const int m = mb * 32 + (lane & 31);
     xoff[mb] = m < M ? ((uint32_t)m * (uint32_t)K + 32u * h) * 2u : OOB;
   }
-  const int ktail = K % TK;  // Q8_0 can end on a half step
+  const int ktail = K % TK;  // the 32-weight block types can end on a half step
   u32x4_t xf[4][4][MB];  // ring: step s in slot s % 4
   auto load_x = [&](int kt, auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
     const int sb = 2 * kt + h;
     const bool in = kt < kt1 && sb < nsub && rok;
     load_raw<QT>(R, row_sub, sb, in, raw[slot]);
-    if constexpr (QT != QT_Q8_0 && (slot & 3) == 0) load_hdr<QT>(R, row_sb, kt >> 2, in, hdr[slot >> 2]);
+    if constexpr (is_kquant(QT) && (slot & 3) == 0) load_hdr<QT>(R, row_sb, kt >> 2, in, hdr[slot >> 2]);
   };
 
   f32x16_t acc[MB];
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
     constexpr int u = decltype(U)::value;
     issue_raw(kt + RING - 1, std::integral_constant<int, (u + RING - 1) % RING>());
     load_x(kt + 2, std::integral_constant<int, (u + 2) & 3>());
-    if constexpr (QT != QT_Q8_0 && (u & 3) == 0) decode_hdr<QT>(hdr[u >> 2], h, sc);
+    if constexpr (is_kquant(QT) && (u & 3) == 0) decode_hdr<QT>(hdr[u >> 2], h, sc);
     uint4 w[4];
     w[0] = dequant_word<QT, XT, 0>(raw[u], sc, u & 3, p.nib);
     w[1] = dequant_word<QT, XT, 1>(raw[u], sc, u & 3, p.nib);
@@ -169,43 +169,45 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
     });
   }
 
-  // partial tiles meet in LDS; thread (mb, lane) adds the nw partials of its 16
-  // accumulators in wavefront order.  Accumulator v holds Y[m][n] for m = mb*32 +
+  // partial tiles meet in LDS; lane `lane` of the wavefront finishing M-block mb adds the
+  // nw partials of its 16 accumulators in wavefront order.  Accumulator v holds Y[m][n] for m = mb*32 +
   // lane%32, n = n0 + 8(v/4) + 4(lane/32) + v%4.
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) red[wave][mb][v][lane] = acc[mb][v];
   __syncthreads();
-  if (tid >= 64 * MB) return;
-  const int mb = tid >> 6;
-  const int m = mb * 32 + (lane & 31);
-  if (m >= M) return;
-  float out[16];
+  // wavefront w finishes M-blocks w, w + nw, ... (a workgroup may have fewer wavefronts
+  // than M-blocks when K is short)
+  for (int mb = wave; mb < MB; mb += nw) {
+    const int m = mb * 32 + (lane & 31);
+    if (m >= M) continue;
+    float out[16];
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    float s = 0.f;
-    for (int w = 0; w < nw; ++w) s += red[w][mb][v][lane];
-    out[v] = s;
-  }
-  const size_t rowbase = (size_t)m * N;
+    for (int v = 0; v < 16; ++v) {
+      float s = 0.f;
+      for (int w = 0; w < nw; ++w) s += red[w][mb][v][lane];
+      out[v] = s;
+    }
+    const size_t rowbase = (size_t)m * N;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int nn = n0 + 8 * q + 4 * (lane >> 5);
-    float v4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      v4[e] = out[4 * q + e] + ((p.bias && nn + e < N) ? load_scalar(p.bias, p.bias_dtype, nn + e) : 0.f);
-    if ((N & 3) == 0 && nn + 3 < N && p.y_dtype != DT_F32) {
-      const uint32_t lo = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[0], v4[1]) : pack2<X_F16>(v4[0], v4[1]);
-      const uint32_t hi = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[2], v4[3]) : pack2<X_F16>(v4[2], v4[3]);
-      *(uint2*)((uint16_t*)p.y + rowbase + nn) = make_uint2(lo, hi);
-    } else if ((N & 3) == 0 && nn + 3 < N) {
-      *(float4*)((float*)p.y + rowbase + nn) = make_float4(v4[0], v4[1], v4[2], v4[3]);
-    } else {
+    for (int q = 0; q < 4; ++q) {
+      const int nn = n0 + 8 * q + 4 * (lane >> 5);
+      float v4[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (nn + e < N) store_scalar(p.y, p.y_dtype, rowbase + nn + e, v4[e]);
+        v4[e] = out[4 * q + e] + ((p.bias && nn + e < N) ? load_scalar(p.bias, p.bias_dtype, nn + e) : 0.f);
+      if ((N & 3) == 0 && nn + 3 < N && p.y_dtype != DT_F32) {
+        const uint32_t lo = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[0], v4[1]) : pack2<X_F16>(v4[0], v4[1]);
+        const uint32_t hi = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[2], v4[3]) : pack2<X_F16>(v4[2], v4[3]);
+        *(uint2*)((uint16_t*)p.y + rowbase + nn) = make_uint2(lo, hi);
+      } else if ((N & 3) == 0 && nn + 3 < N) {
+        *(float4*)((float*)p.y + rowbase + nn) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (nn + e < N) store_scalar(p.y, p.y_dtype, rowbase + nn + e, v4[e]);
+      }
     }
   }
 }
@@ -260,6 +262,8 @@ hipError_t launch_skinny(const RunArgs& a, hipStream_t s) {
   switch (a.L.qtype) {
     case QT_Q4_K: return f16 ? launch_s<QT_Q4_K, X_F16>(sp, s) : launch_s<QT_Q4_K, X_BF16>(sp, s);
     case QT_Q6_K: return f16 ? launch_s<QT_Q6_K, X_F16>(sp, s) : launch_s<QT_Q6_K, X_BF16>(sp, s);
+    case QT_Q4_0: return f16 ? launch_s<QT_Q4_0, X_F16>(sp, s) : launch_s<QT_Q4_0, X_BF16>(sp, s);
+    case QT_Q4_1: return f16 ? launch_s<QT_Q4_1, X_F16>(sp, s) : launch_s<QT_Q4_1, X_BF16>(sp, s);
     default: return f16 ? launch_s<QT_Q8_0, X_F16>(sp, s) : launch_s<QT_Q8_0, X_BF16>(sp, s);
   }
 }

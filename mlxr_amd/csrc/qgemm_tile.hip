@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     const int r = 8 * (MI * wave + i) + (lane >> 3);
     a_voff[i] = (m0 + r < M) ? ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)a_c * 8u) * 2u : OOB;
   }
-  const int ktail = K % TK;  // only Q8_0 can end on a half step (32 of 64)
+  const int ktail = K % TK;  // the 32-weight block types can end on a half step (32 of 64)
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
   const i32x4_t rx = make_srsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
   // Always MI DMA instructions per wavefront and step (steps past the end read zeros
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     const bool in = kt < kend && sb < nsub;
 #pragma unroll
     for (int j = 0; j < 2; ++j) load_raw<QT>(R, row_sub[j], sb, in && rok[j], raw[slot][j]);
-    if constexpr (QT != QT_Q8_0 && slot == 0) {
+    if constexpr (is_kquant(QT) && slot == 0) {
       // first step of a super-block (K-quant steps come in whole super-blocks of four)
 #pragma unroll
       for (int j = 0; j < 2; ++j) load_hdr<QT>(R, row_sb[j], kt >> 2, in && rok[j], hdr[j]);
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   uint4 bf[2][4];
   auto decode_step = [&](auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;  // == step % 4 == sub-block quarter
-    if constexpr (QT != QT_Q8_0 && slot == 0) {
+    if constexpr (is_kquant(QT) && slot == 0) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) decode_hdr<QT>(hdr[j], h, sc[j]);
     }
@@ -463,6 +463,8 @@ hipError_t launch_chunk(const TileParams& tp, int S, int qtype, bool f16, hipStr
   switch (qtype) {
     case QT_Q4_K: return f16 ? launch_q<QT_Q4_K, X_F16>(tp, S, s) : launch_q<QT_Q4_K, X_BF16>(tp, S, s);
     case QT_Q6_K: return f16 ? launch_q<QT_Q6_K, X_F16>(tp, S, s) : launch_q<QT_Q6_K, X_BF16>(tp, S, s);
+    case QT_Q4_0: return f16 ? launch_q<QT_Q4_0, X_F16>(tp, S, s) : launch_q<QT_Q4_0, X_BF16>(tp, S, s);
+    case QT_Q4_1: return f16 ? launch_q<QT_Q4_1, X_F16>(tp, S, s) : launch_q<QT_Q4_1, X_BF16>(tp, S, s);
     default: return f16 ? launch_q<QT_Q8_0, X_F16>(tp, S, s) : launch_q<QT_Q8_0, X_BF16>(tp, S, s);
   }
 }

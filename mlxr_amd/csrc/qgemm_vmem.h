@@ -36,9 +36,9 @@ __device__ __forceinline__ u32x4_t bload16(rsrc_t r, uint32_t voff, uint32_t sof
 
 // VMEM instructions of load_raw / load_hdr (one weight row).
 template <int QT>
-constexpr int raw_loads() { return QT == QT_Q4_K ? 1 : QT == QT_Q6_K ? 2 : 3; }
+constexpr int raw_loads() { return QT == QT_Q4_K ? 1 : QT == QT_Q6_K ? 2 : QT == QT_Q8_0 ? 3 : 2; }
 template <int QT>
-constexpr int hdr_loads() { return QT == QT_Q4_K ? 1 : QT == QT_Q6_K ? 2 : 0; }
+constexpr int hdr_loads() { return QT == QT_Q4_K ? 1 : QT == QT_Q6_K ? 2 : 0; }  // K-quants only
 
 template <int QT>
 __device__ __forceinline__ void load_raw(const rsrc_t* R, uint32_t row_sub, int sb, bool ok, Raw<QT>& r) {
@@ -49,6 +49,12 @@ __device__ __forceinline__ void load_raw(const rsrc_t* R, uint32_t row_sub, int 
   } else if constexpr (QT == QT_Q6_K) {
     r.ql = bload16(R[0], ok ? s * 16u : OOB);
     r.qh = __builtin_amdgcn_raw_buffer_load_b64(R[1], ok ? s * 8u : OOB, 0, 0);
+  } else if constexpr (QT == QT_Q4_0) {
+    r.q = bload16(R[0], ok ? s * 16u : OOB);
+    r.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? s * 2u : OOB, 0, 0);
+  } else if constexpr (QT == QT_Q4_1) {
+    r.q = bload16(R[0], ok ? s * 16u : OOB);
+    r.d = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? s * 4u : OOB, 0, 0);
   } else {
     const uint32_t o = ok ? s * 32u : OOB;
     r.a = bload16(R[0], o);

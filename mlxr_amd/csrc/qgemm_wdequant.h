@@ -8,6 +8,8 @@
 //   Q4_K  fma(d*sc, q, -(dmin*m))       (d*sc, q*d*sc and dmin*m exact; one rounding)
 //   Q6_K  (d*sc) * (q - 32)             (exact; q - 32 formed exactly in fp32)
 //   Q8_0  d * q                         (exact)
+//   Q4_0  (q - 8) * d                   (exact)
+//   Q4_1  fma(q, d, m)                  (q*d exact; one rounding)
 // (the products keep the sign of zero of the GGUF formulas, which an fma with an
 // offset term would not: fma(a, 32, -32a) is +0 for negative a)
 #pragma once
@@ -65,6 +67,27 @@ struct Raw<QT_Q8_0> {
   __device__ void pin_all() {
     pin(a);
     pin(b);
+    pin(d);
+  }
+};
+
+// Q4_0 / Q4_1: one 32-weight block (4 pair-interleaved words) and its scale word
+// (fp16 d, plus fp16 m in the high half for Q4_1).
+template <>
+struct Raw<QT_Q4_0> {
+  u32x4_t q;
+  uint32_t d;
+  __device__ void pin_all() {
+    pin(q);
+    pin(d);
+  }
+};
+template <>
+struct Raw<QT_Q4_1> {
+  u32x4_t q;
+  uint32_t d;
+  __device__ void pin_all() {
+    pin(q);
     pin(d);
   }
 };
@@ -132,6 +155,13 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
     t.u1 = (w >> 4) & nib;
     t.a = s.a[q];
     t.c = s.b[q];
+  } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
+    uint32_t w = r.q[kk];
+    pin(w);
+    t.u0 = w & nib;
+    t.u1 = (w >> 4) & nib;
+    t.a = f16_bits_to_f32(r.d & 0xffffu);
+    t.c = QT == QT_Q4_0 ? 8.f : f16_bits_to_f32(r.d >> 16);
   } else if constexpr (QT == QT_Q6_K) {
     uint32_t lw = r.ql[kk], hv = r.qh[kk >> 1];
     pin(lw);
@@ -154,12 +184,16 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
 
 template <int QT, int XT, int kk, int qq>
 __device__ __forceinline__ uint32_t word_quarter(const WordTmp<QT>& t, uint32_t nib) {
-  if constexpr (QT == QT_Q4_K) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q4_1) {
     // u0 bytes: weights 0, 4, 1, 5; u1 bytes: 2, 6, 3, 7
     const uint32_t v = (qq & 1) ? t.u1 : t.u0;
     const int sh = (qq & 2) ? 8 : 0;
     return pack2<XT>(__builtin_fmaf(t.a, (float)((v >> sh) & 0xffu), t.c),
                      __builtin_fmaf(t.a, (float)((v >> (16 + sh)) & 0xffu), t.c));
+  } else if constexpr (QT == QT_Q4_0) {
+    const uint32_t v = (qq & 1) ? t.u1 : t.u0;
+    const int sh = (qq & 2) ? 8 : 0;
+    return pack2<XT>(((float)((v >> sh) & 0xffu) - t.c) * t.a, ((float)((v >> (16 + sh)) & 0xffu) - t.c) * t.a);
   } else if constexpr (QT == QT_Q6_K) {
     constexpr int rs = 8 * (kk & 1) + 2 * qq - 4;
     const uint32_t hs = rs >= 0 ? (t.u1 >> rs) : (t.u1 << (-rs));
@@ -192,6 +226,12 @@ __device__ __forceinline__ void load_sub_plain(const PlanePtrs& P, int K, int n,
   if constexpr (QT == QT_Q4_K) {
     r.q = *(const u32x4_t*)(P.p[0] + s * 16);
     h.h = *(const u32x4_t*)(P.p[1] + g * 16);
+  } else if constexpr (QT == QT_Q4_0) {
+    r.q = *(const u32x4_t*)(P.p[0] + s * 16);
+    r.d = *(const uint16_t*)(P.p[1] + s * 2);
+  } else if constexpr (QT == QT_Q4_1) {
+    r.q = *(const u32x4_t*)(P.p[0] + s * 16);
+    r.d = *(const uint32_t*)(P.p[1] + s * 4);
   } else if constexpr (QT == QT_Q6_K) {
     r.ql = *(const u32x4_t*)(P.p[0] + s * 16);
     r.qh = *(const u32x2_t*)(P.p[1] + s * 8);

@@ -91,7 +91,8 @@ int mlxr_synth_gguf(int qtype, int N, int K, uint64_t seed, void* out_host) {
   int rc = mlxr_qgemm_gguf_size(qtype, N, K, &bytes);
   if (rc) return rc;
   if (!out_host) return MLXR_E_INVALID;
-  if (qtype != MLXR_Q8_0 && qtype != MLXR_Q4_K && qtype != MLXR_Q6_K) return MLXR_E_UNSUPPORTED;
+  if (qtype != MLXR_Q8_0 && qtype != MLXR_Q4_K && qtype != MLXR_Q6_K && qtype != MLXR_Q4_0 && qtype != MLXR_Q4_1)
+    return MLXR_E_UNSUPPORTED;
   const int g = mlxr_qgemm_group_size(qtype);
   if (K % g) return MLXR_E_SHAPE;
   SplitMix64 r(seed);
@@ -102,6 +103,15 @@ int mlxr_synth_gguf(int qtype, int N, int K, uint64_t seed, void* out_host) {
       put16(p, f32_to_f16((float)(fabs(r.normal()) * 0.02 / 127.0)));
       for (int i = 0; i < 32; ++i) p[2 + i] = (uint8_t)(int8_t)((int)r.below(255) - 127);
       p += 34;
+    } else if (qtype == MLXR_Q4_0) {
+      put16(p, f32_to_f16((float)(fabs(r.normal()) * 2e-3)));
+      fill_bytes(r, p + 2, 16);
+      p += 18;
+    } else if (qtype == MLXR_Q4_1) {
+      put16(p, f32_to_f16((float)(fabs(r.normal()) * 2e-3)));
+      put16(p + 2, f32_to_f16((float)(r.normal() * 8e-3)));
+      fill_bytes(r, p + 4, 16);
+      p += 20;
     } else if (qtype == MLXR_Q4_K) {
       put16(p, f32_to_f16((float)(fabs(r.normal()) * 1e-3)));
       put16(p + 2, f32_to_f16((float)(fabs(r.normal()) * 1e-3)));

@@ -10,6 +10,10 @@
  *   - fp16 -> fp32                core/kernels/primitives/q_gemm_dequant_primitive.mm:141-165
  *   - block layouts               q_gemm_dequant_primitive.mm:40-57, q_gemm_dequant.metal:97-131
  *   - Q8_0 dequant                q_gemm_dequant_primitive.mm:218-225 (identical formula)
+ *   - Q4_0 / Q4_1 dequant         q_gemm_dequant_primitive.mm:189-216 (same formulas,
+ *                                 (q - 8) * d and q * d + m, but in the GGUF element order;
+ *                                 the reference's interleaved order is kept as
+ *                                 orc_dequant_refcpu_q4 and its relation pinned in tests)
  *   - Q4_K / Q6_K dequant         canonical GGUF block_q4_K / block_q6_K semantics (the
  *                                 reference's only K-quant routines are the Metal ones at
  *                                 q_gemm_dequant.metal:214-286, which are not GGUF-conformant;
@@ -159,6 +163,50 @@ static void dq_q8_0(const uint8_t* blk, float* y) {
     for (int i = 0; i < 32; i++) y[i] = (float)qs[i] * d;
 }
 
+/* block_q4_0 = { fp16 d; u8 qs[16]; }  GGUF order: byte j holds element j (low nibble) and
+ * element j+16 (high nibble).  w = (q - 8) * fp32(d), exact (q - 8 has 4 bits). */
+static void dq_q4_0(const uint8_t* blk, float* y) {
+    float d = orc_f16_to_f32(rd16(blk));
+    const uint8_t* qs = blk + 2;
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)((int)(qs[j] & 0x0f) - 8) * d;
+        y[j + 16] = (float)((int)(qs[j] >> 4) - 8) * d;
+    }
+}
+
+/* block_q4_1 = { fp16 d; fp16 m; u8 qs[16]; }  GGUF order as Q4_0.  w = q * d + m: the
+ * product is exact, so the one rounding is the addition (same with or without fma). */
+static void dq_q4_1(const uint8_t* blk, float* y) {
+    float d = orc_f16_to_f32(rd16(blk));
+    float m = orc_f16_to_f32(rd16(blk + 2));
+    const uint8_t* qs = blk + 4;
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)(qs[j] & 0x0f) * d + m;
+        y[j + 16] = (float)(qs[j] >> 4) * d + m;
+    }
+}
+
+/* The reference's own CPU routines dequant_q4_0_cpu / dequant_q4_1_cpu
+ * (q_gemm_dequant_primitive.mm:189-216) read the nibbles interleaved: byte i holds
+ * elements 2i (low) and 2i+1 (high).  Same values, different element order from GGUF;
+ * kept to document that divergence (tests pin the permutation between the two). */
+int orc_dequant_refcpu_q4(int qtype, const uint8_t* blk, float* y) {
+    if (qtype != Q4_0 && qtype != Q4_1) return -1;
+    float d = orc_f16_to_f32(rd16(blk));
+    float m = qtype == Q4_1 ? orc_f16_to_f32(rd16(blk + 2)) : 0.0f;
+    const uint8_t* qs = blk + (qtype == Q4_1 ? 4 : 2);
+    for (int i = 0; i < 16; i++) {
+        if (qtype == Q4_0) {
+            y[2 * i] = (float)((int)(qs[i] & 0x0f) - 8) * d;
+            y[2 * i + 1] = (float)((int)(qs[i] >> 4) - 8) * d;
+        } else {
+            y[2 * i] = (float)(qs[i] & 0x0f) * d + m;
+            y[2 * i + 1] = (float)(qs[i] >> 4) * d + m;
+        }
+    }
+    return 0;
+}
+
 /* 6-bit scale and min of sub-block j (0..7) from the 12 packed bytes. */
 void orc_q4k_scale_min(const uint8_t* s, int j, int* sc, int* m) {
     if (j < 4) {
@@ -226,7 +274,7 @@ static void dq_q6_k(const uint8_t* blk, float* y) {
  * Returns 0 on success, -1 for an unsupported type or K not a block multiple. */
 int orc_dequant(int qtype, int N, int K, const uint8_t* w, float* out) {
     int g = orc_block_elems(qtype), bb = orc_block_bytes(qtype);
-    if (g == 0 || K % g != 0 || (qtype != Q8_0 && qtype != Q4_K && qtype != Q6_K)) return -1;
+    if (g == 0 || K % g != 0) return -1;
     int nb = K / g;
 #pragma omp parallel for schedule(static)
     for (int n = 0; n < N; n++) {
@@ -234,6 +282,8 @@ int orc_dequant(int qtype, int N, int K, const uint8_t* w, float* out) {
             const uint8_t* blk = w + ((size_t)n * nb + b) * bb;
             float* y = out + (size_t)n * K + (size_t)b * g;
             if (qtype == Q8_0) dq_q8_0(blk, y);
+            else if (qtype == Q4_0) dq_q4_0(blk, y);
+            else if (qtype == Q4_1) dq_q4_1(blk, y);
             else if (qtype == Q4_K) dq_q4_k(blk, y);
             else dq_q6_k(blk, y);
         }

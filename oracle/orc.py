@@ -39,6 +39,7 @@ def lib():
         l.orc_eval_cpu.argtypes = [I, I, I, I, P, P, P, P]
         l.orc_eval_cpu_cols.argtypes = [I, I, I, I, I, I, P, P, P, P]
         l.orc_gemm_f64.argtypes = [I, I, I, I, P, P, P, I, I, I, P]
+        l.orc_dequant_refcpu_q4.argtypes = [I, P, P]
         _lib = l
     return _lib
 
@@ -65,6 +66,14 @@ def dequant(qtype, N, K, w):
     rc = lib().orc_dequant(int(qtype), N, K, _p(np.ascontiguousarray(w)), _p(out))
     if rc:
         raise ValueError(f"orc_dequant rc={rc}")
+    return out
+
+
+def dequant_refcpu_q4(qtype, block):
+    """The reference CPU routine's element order for one Q4_0/Q4_1 block (32 floats)."""
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    out = np.empty(32, np.float32)
+    assert lib().orc_dequant_refcpu_q4(int(qtype), _p(b), _p(out)) == 0
     return out
 
 

@@ -78,6 +78,14 @@ def planes(qtype, N, K, gguf):
             hw[..., e >> 4] |= hs[..., e] << np.uint32(q6h_shift(e))
         return [lw.view(np.uint8).reshape(-1), hw.view(np.uint8).reshape(-1),
                 b[..., 192:208].reshape(-1).copy(), b[..., 208:210].reshape(-1).copy()]
+    if qtype in (0, 1):  # Q4_0 / Q4_1: byte j holds elements j (low) and j + 16 (high)
+        nb = K // 32
+        hb = 2 if qtype == 0 else 4
+        b = g.reshape(N, nb, hb + 16)
+        qs = b[..., hb:]
+        nib = np.concatenate([qs & 15, qs >> 4], axis=-1).reshape(N, nb, 1, 32)
+        words = _words_from_nibbles(nib)  # [N, nb, 1, 4]
+        return [words.view(np.uint8).reshape(-1), b[..., 0:hb].reshape(-1).copy()]
     if qtype == 2:  # Q8_0
         nb = K // 32
         b = g.reshape(N, nb, 34)

@@ -15,11 +15,15 @@ from mlxr_amd import qgemm
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HDR = os.path.join(ROOT, "include", "mlxr_qgemm.h")
+C_HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+             if h.startswith("mlxr_") and h.endswith(".h")]
 
 
 def test_exports_every_declared_symbol():
-    names = set(re.findall(r"\b(mlxr_\w+)\s*\(", open(HDR).read()))
-    assert len(names) >= 13
+    names = set()
+    for h in C_HEADERS:
+        names |= set(re.findall(r"\b(mlxr_\w+)\s*\(", open(h).read()))
+    assert len(names) >= 30
     lib = ctypes.CDLL(qgemm.LIB_PATH)
     for n in sorted(names):
         assert hasattr(lib, n), n
@@ -44,7 +48,7 @@ def test_metadata_matches_reference_helpers():
     assert mx.gguf_size(mx.QuantType.Q8_0, 2048, 2048) == 4456448
     assert mx.gguf_size(mx.QuantType.Q4_0, 1, 32) == 18  # reference parser test: Q4_0 = 18 B / 32
     assert mx.get_bytes_per_weight(mx.QuantType.Q4_K) < 1.0
-    for qt, N, K in ((3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048), (3, 3, 256)):
+    for qt, N, K in ((3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048), (3, 3, 256), (0, 5, 96), (1, 7, 4096)):
         ps, gs = mx.packed_size(qt, N, K), mx.gguf_size(qt, N, K)
         assert gs <= ps < gs + 4 * 256  # same bytes, planes 256-byte aligned
 
@@ -57,8 +61,8 @@ def _err(fn):
 
 def test_error_paths():
     L = mx.lib()
-    e = _err(lambda: mx.packed_size(mx.QuantType.Q4_0, 16, 256))
-    assert e.code == -2 and "Unsupported quantization type Q4_0" in str(e)
+    e = _err(lambda: mx.packed_size(mx.QuantType.Q5_K, 16, 256))
+    assert e.code == -2 and "Unsupported quantization type Q5_K" in str(e)
     e = _err(lambda: mx.packed_size(mx.QuantType.Q4_K, 16, 300))
     assert e.code == -3 and "multiple" in str(e)
     e = _err(lambda: mx.packed_size(mx.QuantType.Q6_K, 0, 256))
@@ -80,13 +84,13 @@ def test_error_paths():
 
 def test_last_error_is_thread_local():
     L = mx.lib()
-    assert L.mlxr_qgemm_packed_size(0, 1, 32, ctypes.byref(ctypes.c_size_t())) == -2
+    assert L.mlxr_qgemm_packed_size(10, 1, 256, ctypes.byref(ctypes.c_size_t())) == -2
     seen = []
     t = threading.Thread(target=lambda: seen.append(L.mlxr_qgemm_last_error()))
     t.start()
     t.join()
     assert seen == [b""]
-    assert b"Q4_0" in L.mlxr_qgemm_last_error()
+    assert b"Q5_K" in L.mlxr_qgemm_last_error()
 
 
 def test_python_operator_shape_checks():

@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 5e-3
 Q4K, Q6K, Q80 = mx.QuantType.Q4_K, mx.QuantType.Q6_K, mx.QuantType.Q8_0
+Q40, Q41 = mx.QuantType.Q4_0, mx.QuantType.Q4_1
 
 
 def _dev_bytes(torch, arr, device):
@@ -34,7 +35,8 @@ def _packed(torch, qt, N, K, seed, device):
     return w, mx.pack_weights(w, N, K, qt, device=device)
 
 
-@pytest.mark.parametrize("qt,N,K", [(Q4K, 64, 1024), (Q6K, 48, 768), (Q80, 40, 2048), (Q4K, 3, 256)])
+@pytest.mark.parametrize("qt,N,K", [(Q4K, 64, 1024), (Q6K, 48, 768), (Q80, 40, 2048), (Q4K, 3, 256), (Q40, 33, 96),
+                                    (Q41, 40, 1024)])
 def test_pack_bytes_match_layout(cuda, qt, N, K):
     import torch
     w = mx.synth_gguf(qt, N, K, 11)
@@ -48,7 +50,8 @@ def test_pack_bytes_match_layout(cuda, qt, N, K):
     assert off == pw.nbytes
 
 
-@pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 256, 2048), (Q4K, 1, 256)])
+@pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 256, 2048), (Q4K, 1, 256),
+                                    (Q40, 128, 2048), (Q41, 96, 4128)])
 def test_dequant_f32_bit_exact(cuda, qt, N, K):
     import torch
     w, pw = _packed(torch, qt, N, K, 21, cuda)
@@ -57,7 +60,8 @@ def test_dequant_f32_bit_exact(cuda, qt, N, K):
     np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 64, 2048)])
+@pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 64, 2048), (Q40, 64, 1024),
+                                    (Q41, 64, 1056)])
 def test_dequant_bf16_rne_bit_exact(cuda, qt, N, K):
     import torch
     w, pw = _packed(torch, qt, N, K, 22, cuda)
@@ -72,6 +76,8 @@ GEMV_CASES = [
     (Q4K, 16, 96, 768), (Q4K, 33, 64, 1024), (Q4K, 64, 80, 512),
     (Q6K, 1, 300, 2048), (Q6K, 5, 128, 1280), (Q6K, 64, 64, 512),
     (Q80, 1, 256, 2048), (Q80, 2, 100, 96), (Q80, 40, 64, 1024),
+    (Q40, 1, 300, 2048), (Q40, 3, 64, 96), (Q40, 12, 128, 1024), (Q41, 1, 256, 4096), (Q41, 4, 200, 160),
+    (Q41, 64, 64, 512),
 ]
 
 
@@ -85,13 +91,18 @@ def test_gemv_matches_oracle(cuda, qt, M, N, K, xdt):
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf)
     err = orc.normwise_rel_err(y.cpu().numpy(), ref)
     assert err <= TOL, err
-    # the GEMV accumulates exact products in fp32: far tighter than the contract
-    assert err <= 1e-5, err
+    # the GEMV accumulates in fp32 (magic-offset dot products, one cancellation per
+    # sub-block): far tighter than the contract
+    assert err <= 3e-5, err
 
 
 MFMA_CASES = [
     (Q4K, 128, 256, 1024), (Q4K, 130, 200, 512), (Q4K, 1, 128, 256), (Q4K, 256, 384, 2048),
     (Q6K, 128, 128, 1024), (Q6K, 200, 96, 512), (Q80, 128, 160, 1024), (Q80, 77, 64, 96),
+    (Q40, 128, 256, 1024), (Q40, 33, 96, 96), (Q40, 8, 512, 2048), (Q41, 160, 128, 1056), (Q41, 64, 300, 4096),
+    (Q41, 5, 64, 160),
+    # one wavefront per workgroup (short K) with two M-blocks: every row must be stored
+    (Q4K, 40, 64, 256), (Q6K, 64, 32, 512), (Q80, 33, 64, 64),
 ]
 
 
@@ -228,6 +239,7 @@ def test_mfma_chunked_launches(cuda, monkeypatch):
 
 
 @pytest.mark.parametrize("qt,M,N,K,ydt", [(Q4K, 512, 1024, 4096, "bf16"), (Q6K, 256, 1000, 2048, "f32"),
+                                          (Q41, 300, 512, 4096, "bf16"),
                                           (Q80, 130, 384, 1056, "f16"), (Q4K, 2048, 1024, 4096, "f32")])
 def test_mfma_split_k(cuda, qt, M, N, K, ydt):
     """Split-K through the C ABI: mlxr_qgemm_run_ws with the workspace size the library

@@ -46,20 +46,29 @@ def decode(qt, N, K, planes):
         ds = d[..., None, None] * sc                  # [N, nsb, 8, 2]
         w = np.repeat(ds, 16, axis=-1) * q.astype(np.float32)
         return w.reshape(N, K)
+    if qt in (0, 1):
+        nb = K // 32
+        q = _nibbles(planes[0].view(np.uint32).reshape(N, nb, 4)).astype(np.float32)
+        hdr = planes[1].view(np.float16).reshape(N, nb, 1 if qt == 0 else 2).astype(np.float32)
+        d = hdr[..., 0:1]
+        if qt == 0:
+            return ((q - np.float32(8)) * d).reshape(N, K)  # exact
+        return (q * d + hdr[..., 1:2]).reshape(N, K)      # product exact, one rounding
     nb = K // 32
     q = planes[0].view(np.int8).reshape(N, nb, 32).astype(np.float32)
     d = planes[1].view(np.float16).reshape(N, nb).astype(np.float32)
     return (q * d[..., None]).reshape(N, K)
 
 
-@pytest.mark.parametrize("qt,N,K", [(3, 8, 1024), (4, 6, 768), (2, 5, 256), (3, 1, 256)])
+@pytest.mark.parametrize("qt,N,K", [(3, 8, 1024), (4, 6, 768), (2, 5, 256), (3, 1, 256), (0, 7, 96), (1, 5, 320)])
 def test_packed_layout_decodes_to_oracle(qt, N, K):
     w = mx.synth_gguf(qt, N, K, 100 + qt)
     got = decode(qt, N, K, packref.planes(qt, N, K, w))
     np.testing.assert_array_equal(got.view(np.uint32), orc.dequant(qt, N, K, w).view(np.uint32))
 
 
-@pytest.mark.parametrize("qt,N,K", [(3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048)])
+@pytest.mark.parametrize("qt,N,K", [(3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048), (0, 4096, 4096),
+                                    (1, 1024, 2080)])
 def test_packed_size_is_gguf_size(qt, N, K):
     planes = packref.planes(qt, N, K, np.zeros(mx.gguf_size(qt, N, K), np.uint8))
     assert sum(p.size for p in planes) == mx.gguf_size(qt, N, K)

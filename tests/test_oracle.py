@@ -136,6 +136,60 @@ def test_q8_0_known_answers():
         np.testing.assert_array_equal(got, qs.astype(np.float32) * np.float32(d))
 
 
+# ---------------------------------------------------------------- Q4_0 / Q4_1
+
+def q4_block(qt, d_bits, qs, m_bits=0):
+    hb = np.array([d_bits] if qt == 0 else [d_bits, m_bits], np.uint16).view(np.uint8)
+    return np.concatenate([hb, np.asarray(qs, np.uint8)])
+
+
+def test_q4_0_element_order_and_values():
+    # byte j = lo | hi << 4 with lo = j, hi = 15 - j: element j = j - 8, element j+16 = 7 - j
+    qs = np.array([j | ((15 - j) << 4) for j in range(16)], np.uint8)
+    for d in (1.0, -0.5, 65504.0, 2.0 ** -24, 0.0):
+        got = orc.dequant(0, 1, 32, q4_block(0, f16(d), qs))[0]
+        want = np.array([j - 8 for j in range(16)] + [7 - j for j in range(16)], np.float32) * np.float32(d)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))  # incl. sign of zero
+
+
+def test_q4_1_element_order_and_values():
+    qs = np.array([j | ((15 - j) << 4) for j in range(16)], np.uint8)
+    for d, m in ((1.0, 0.0), (0.25, -3.0), (2.0 ** -14, 1.5), (0.0, -2.0), (3.0, -0.0)):
+        got = orc.dequant(1, 1, 32, q4_block(1, f16(d), qs, f16(m)))[0]
+        q = np.array(list(range(16)) + [15 - j for j in range(16)], np.float64)
+        want = (q * d + m).astype(np.float32)  # q*d is exact, so the fp64 sum rounds once
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qt", [0, 1])
+def test_q4_gguf_order_vs_reference_cpu_order(qt):
+    """The reference's CPU routines (q_gemm_dequant_primitive.mm:189-216) give the same
+    32 values in interleaved order: theirs[2i] = gguf[i], theirs[2i+1] = gguf[i+16]."""
+    blk = mx.synth_gguf(qt, 1, 32, 9 + qt)
+    g = orc.dequant(qt, 1, 32, blk)[0]
+    r = orc.dequant_refcpu_q4(qt, blk)
+    np.testing.assert_array_equal(r[0::2], g[:16])
+    np.testing.assert_array_equal(r[1::2], g[16:])
+
+
+@pytest.mark.parametrize("qt", [0, 1])
+def test_q4_matches_elementwise_decoder(qt):
+    N, K = 3, 128
+    w = mx.synth_gguf(qt, N, K, 40 + qt)
+    hb = 2 if qt == 0 else 4
+    b = w.reshape(N, K // 32, hb + 16)
+    out = np.empty((N, K), np.float32)
+    for n in range(N):
+        for blk in range(K // 32):
+            d = np.float32(b[n, blk, 0:2].view(np.float16)[0])
+            m = np.float32(b[n, blk, 2:4].view(np.float16)[0]) if qt == 1 else None
+            for e in range(32):
+                byte = int(b[n, blk, hb + (e % 16)])
+                q = (byte & 15) if e < 16 else (byte >> 4)
+                out[n, 32 * blk + e] = np.float32(q - 8) * d if qt == 0 else np.float32(np.float64(q) * d + m)
+    np.testing.assert_array_equal(orc.dequant(qt, N, K, w).view(np.uint32), out.view(np.uint32))
+
+
 # ----------------------------------------------------------------------- Q4_K
 
 # One-hot scale bits, derived by hand from the GGUF 12-byte packing: sub-blocks 0..3 keep
@@ -354,5 +408,5 @@ def test_gemm_linearity():
 
 
 def test_unsupported_types_rejected():
-    assert orc.lib().orc_dequant(0, 1, 32, None, None) == -1  # Q4_0 has no oracle here
+    assert orc.lib().orc_dequant(10, 1, 256, None, None) == -1  # Q5_K has no oracle here
     assert orc.lib().orc_dequant(Q4K, 1, 300, None, None) == -1  # K not a block multiple
