@@ -11,8 +11,8 @@
 //
 //  * Activations (shared by the four wavefronts) go HBM -> LDS by buffer_load ... lds
 //    (no VGPR staging), four stages, three steps ahead.  A BM x 64 stage has 128-byte
-//    rows; the 16-byte chunk c of row r is stored at position c ^ (r & 7), so the
-//    fragment reads of eight consecutive rows hit eight different 16-byte bank groups.
+//    rows; the 16-byte chunk c of row r is stored at position c ^ swz(r), so the
+//    fragment reads of sixteen consecutive rows hit sixteen different 16-byte bank groups.
 //    The DMA is issued from inline assembly, so the compiler (which would otherwise wait
 //    for every outstanding load before each LDS read) leaves the stage waits to the
 //    exact vmcnt values computed from the fixed issue order; the weight loads are
@@ -71,6 +71,16 @@ struct TileParams {
   uint32_t nib;  // 0x0F0F0F0F, passed at run time (keeps the byte converts)
 };
 
+// LDS position of 16-byte chunk c of activation row r in a stage: c ^ swz(r).  Fragment
+// reads take rows r .. r+15 of one chunk column per 16-lane phase; with 128-byte rows
+// and 64 four-byte banks, row r lands in bank group 8(r & 1) + (c ^ swz(r)), so swz must
+// be a bijection on the eight even and on the eight odd rows of an aligned group of 16.
+#ifndef MLXR_SWZ_LEGACY
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+#else
+__device__ __forceinline__ int swz(int r) { return r & 7; }
+#endif
+
 template <int XT>
 __device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f32x16_t& c) {
   if constexpr (XT == X_BF16)
@@ -123,12 +133,14 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
 
   // --- activations: LDS DMA.  Wave w fills slot blocks MI*w .. MI*w+MI-1 of a stage
   // (1 KiB = 8 rows each); lane l of block b brings row 8b + l/8, global chunk
-  // (l%8) ^ (l/8), to chunk position l%8.  Rows past M read zeros.
+  // (l%8) ^ swz(row), to chunk position l%8.  Rows past M read zeros.
   uint32_t a_voff[MI];
-  const int a_c = (lane & 7) ^ (lane >> 3);
+  bool a_hi[MI];  // this lane's chunk is in the upper half of the step (K offset >= 32)
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     const int r = 8 * (MI * wave + i) + (lane >> 3);
+    const int a_c = (lane & 7) ^ swz(r);
+    a_hi[i] = a_c >= 4;
     a_voff[i] = (m0 + r < M) ? ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)a_c * 8u) * 2u : OOB;
   }
   const int ktail = K % TK;  // the 32-weight block types can end on a half step (32 of 64)
@@ -138,12 +150,12 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   // into a stage nobody reads), so the wait counts below are exact.
   auto issue_a = [&](int kt) {
     const bool live = kt < kend;
-    const bool cut = ktail != 0 && kt == nkt - 1 && a_c * 8 >= ktail;
+    const bool last_half = ktail != 0 && kt == nkt - 1;  // ktail is 32 here
     const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane(kt * (TK * 2));
     const uint32_t dst = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * A_STAGE + wave * MI * 1024);
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      const uint32_t vo = (live && !cut) ? a_voff[i] : OOB;
+      const uint32_t vo = (live && !(last_half && a_hi[i])) ? a_voff[i] : OOB;
       const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + i * 1024));
       // M0 holds the LDS destination; nothing else in this kernel uses M0 (DS
       // instructions on gfx9+ do not), so clobbering it is safe here.
@@ -215,7 +227,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   auto read_a = [&](int stage, int f) -> uint4 {
     const int kk = f / MI, i = f % MI;
     const int r = 32 * i + fr;
-    const int c = (4 * h + kk) ^ (r & 7);
+    const int c = (4 * h + kk) ^ swz(r);
     return *(const uint4*)(lds + stage * A_STAGE + r * 128 + c * 16);
   };
 
@@ -382,39 +394,52 @@ int device_cus() {
   return 256;
 }
 
-// 256-row tiles, unless they would leave more than a quarter of the CUs idle and
-// 128-row tiles give more of them (MLXR_MFMA_BM = 128 / 256 forces one).
-int pick_bm(int M, int N) {
-  static const int force = getenv("MLXR_MFMA_BM") ? atoi(getenv("MLXR_MFMA_BM")) : 0;
-  if (force == 128 || force == 256) return force;
-  const long tn = (N + TN - 1) / TN;
-  const long t256 = ((M + 255) / 256) * tn, t128 = ((M + 127) / 128) * tn;
-  return (4 * t256 < 3 * (long)device_cus() && t128 > t256) ? 128 : 256;
-}
-
-// Split-K plan: when the tiles of [M, N] leave more than a quarter of the CUs idle, K is
-// split into S ranges of whole super-block groups (at least eight steps each) so that
-// about one workgroup per CU runs; S <= 8.
+// Tile rows and K split of a launch, from a small cost model in units of one 256-row
+// tile step: a 128-row tile step costs 0.64 of it (the weight dequant is shared by half
+// the rows); a round of workgroups costs its steps plus 0.8 (prologue, epilogue); a
+// split launch adds the reduce kernel, about 3 us plus its partial-sum traffic at
+// ~5 TB/s (one 256-row step is ~1.86 us).  Splits are whole groups of four steps (a
+// super-block), at least eight steps each, at most eight splits, and only with a
+// workspace of S*M*N*4 bytes.  MLXR_MFMA_BM / MLXR_MFMA_SPLIT force a choice.
 struct SplitPlan {
   int bm, tiles, S, kps;
 };
-SplitPlan plan_split(int M, int N, int K) {
-  SplitPlan sp;
-  sp.bm = pick_bm(M, N);
-  sp.tiles = ((M + sp.bm - 1) / sp.bm) * ((N + TN - 1) / TN);
+SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
+  static const int force_bm = getenv("MLXR_MFMA_BM") ? atoi(getenv("MLXR_MFMA_BM")) : 0;
+  static const int force_s = getenv("MLXR_MFMA_SPLIT") ? atoi(getenv("MLXR_MFMA_SPLIT")) : 0;
   const int nkt = (K + TK - 1) / TK, cus = device_cus();
-  int S = 1;
-  if (4 * sp.tiles < 3 * cus) S = std::max(1, std::min({(cus + sp.tiles - 1) / sp.tiles, 8, nkt / 8}));
-  static const int force = getenv("MLXR_MFMA_SPLIT") ? atoi(getenv("MLXR_MFMA_SPLIT")) : 0;
-  if (force >= 1) S = std::max(1, std::min(force, (nkt + 3) / 4));
-  sp.kps = (((nkt + S - 1) / S) + 3) / 4 * 4;
-  sp.S = (nkt + sp.kps - 1) / sp.kps;
-  return sp;
+  const long tn = (N + TN - 1) / TN;
+  SplitPlan best{256, 0, 1, 0};
+  double best_t = 1e30;
+  for (int bm : {256, 128}) {
+    if ((force_bm == 128 || force_bm == 256) && bm != force_bm) continue;
+    const long tiles = ((M + bm - 1) / bm) * tn;
+    for (int S = 1; S <= 8; ++S) {
+      if (force_s >= 1 && S != std::min(force_s, (nkt + 3) / 4)) continue;
+      const int kps = (((nkt + S - 1) / S) + 3) / 4 * 4;
+      const int Sr = (nkt + kps - 1) / kps;  // splits actually used
+      if (Sr != S) continue;
+      if (S > 1 && ((force_s < 1 && kps < 8) || (size_t)S * (size_t)M * (size_t)N * 4u > ws_bytes)) continue;
+      const long rounds = (tiles * S + cus - 1) / cus;
+      double t = (double)rounds * (kps * (bm == 256 ? 1.0 : 0.64) + 0.8);
+      if (S > 1) t += (3.0 + (double)S * M * N * 8.0 / 5e6) / 1.86;
+      if (t < best_t) {
+        best_t = t;
+        best = SplitPlan{bm, (int)tiles, S, kps};
+      }
+    }
+  }
+  if (best.kps == 0) {  // nothing qualified (a forced split without workspace): no split
+    best.bm = force_bm == 128 ? 128 : 256;
+    best.tiles = (int)(((M + best.bm - 1) / best.bm) * tn);
+    best.S = 1;
+    best.kps = nkt;
+  }
+  return best;
 }
 
 template <int QT, int XT>
-hipError_t launch_q(TileParams tp, int S, hipStream_t s) {
-  const int bm = pick_bm(tp.M, tp.N);
+hipError_t launch_q(TileParams tp, int bm, int S, hipStream_t s) {
   tp.tiles_m = (tp.M + bm - 1) / bm;
   tp.tiles_n = (tp.N + TN - 1) / TN;
   const int ntiles = tp.tiles_m * tp.tiles_n;
@@ -459,13 +484,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-hipError_t launch_chunk(const TileParams& tp, int S, int qtype, bool f16, hipStream_t s) {
+hipError_t launch_chunk(const TileParams& tp, int bm, int S, int qtype, bool f16, hipStream_t s) {
   switch (qtype) {
-    case QT_Q4_K: return f16 ? launch_q<QT_Q4_K, X_F16>(tp, S, s) : launch_q<QT_Q4_K, X_BF16>(tp, S, s);
-    case QT_Q6_K: return f16 ? launch_q<QT_Q6_K, X_F16>(tp, S, s) : launch_q<QT_Q6_K, X_BF16>(tp, S, s);
-    case QT_Q4_0: return f16 ? launch_q<QT_Q4_0, X_F16>(tp, S, s) : launch_q<QT_Q4_0, X_BF16>(tp, S, s);
-    case QT_Q4_1: return f16 ? launch_q<QT_Q4_1, X_F16>(tp, S, s) : launch_q<QT_Q4_1, X_BF16>(tp, S, s);
-    default: return f16 ? launch_q<QT_Q8_0, X_F16>(tp, S, s) : launch_q<QT_Q8_0, X_BF16>(tp, S, s);
+    case QT_Q4_K: return f16 ? launch_q<QT_Q4_K, X_F16>(tp, bm, S, s) : launch_q<QT_Q4_K, X_BF16>(tp, bm, S, s);
+    case QT_Q6_K: return f16 ? launch_q<QT_Q6_K, X_F16>(tp, bm, S, s) : launch_q<QT_Q6_K, X_BF16>(tp, bm, S, s);
+    case QT_Q4_0: return f16 ? launch_q<QT_Q4_0, X_F16>(tp, bm, S, s) : launch_q<QT_Q4_0, X_BF16>(tp, bm, S, s);
+    case QT_Q4_1: return f16 ? launch_q<QT_Q4_1, X_F16>(tp, bm, S, s) : launch_q<QT_Q4_1, X_BF16>(tp, bm, S, s);
+    default: return f16 ? launch_q<QT_Q8_0, X_F16>(tp, bm, S, s) : launch_q<QT_Q8_0, X_BF16>(tp, bm, S, s);
   }
 }
 
@@ -492,9 +517,11 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   const PlanePtrs P = plane_ptrs(a.L, a.packed);
   const size_t ye = dtype_bytes(a.y_dtype), be = dtype_bytes(a.bias_dtype);
   // split-K (single-chunk problems with a large enough workspace only)
+  // the plan for an unlimited workspace, used only if the caller's workspace holds it
+  // (so a given shape either takes that plan or the unsplit one, never a third)
   SplitPlan sp{0, 0, 1, 0};
   if (a.ws && M <= Mc && N <= Nc) {
-    sp = plan_split(M, N, K);
+    sp = plan_split(M, N, K, ~(size_t)0);
     if (sp.S > 1 && (size_t)sp.S * (size_t)M * (size_t)N * 4u > a.ws_bytes) sp.S = 1;
   }
   if (sp.S > 1) {
@@ -516,7 +543,7 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
     tp.kps = sp.kps;
     tp.ws = (float*)a.ws;
     tp.ws_split = (size_t)M * (size_t)N;
-    hipError_t e = launch_chunk(tp, sp.S, a.L.qtype, a.x_dtype == DT_F16, s);
+    hipError_t e = launch_chunk(tp, sp.bm, sp.S, a.L.qtype, a.x_dtype == DT_F16, s);
     if (e != hipSuccess) return e;
     const size_t total = (size_t)M * (size_t)N;
     if ((N & 3) == 0) {
@@ -549,7 +576,8 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
       tp.kps = (K + TK - 1) / TK;
       tp.ws = nullptr;
       tp.ws_split = 0;
-      const hipError_t e = launch_chunk(tp, 1, a.L.qtype, a.x_dtype == DT_F16, s);
+      const int bm = plan_split(tp.M, tp.N, K, 0).bm;
+      const hipError_t e = launch_chunk(tp, bm, 1, a.L.qtype, a.x_dtype == DT_F16, s);
       if (e != hipSuccess) return e;
     }
   }
@@ -558,7 +586,7 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
 
 size_t mfma_workspace_bytes(int M, int N, int K) {
   if (M <= 64 || (size_t)M * (size_t)K * 2u >= ((size_t)1 << 31)) return 0;
-  const SplitPlan sp = plan_split(M, N, K);
+  const SplitPlan sp = plan_split(M, N, K, ~(size_t)0);
   return sp.S > 1 ? (size_t)sp.S * (size_t)M * (size_t)N * 4u : 0;
 }
 
