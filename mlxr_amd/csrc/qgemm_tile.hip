@@ -22,8 +22,9 @@
 //    (n, h) then owns exactly sub-block h of the step for its weight rows n and n + 32,
 //    dequantizes those 32 weights in registers and uses word kk of the result as the B
 //    fragment of MFMA kk.  Per-super-block header work (d, dmin, six-bit scales) is done
-//    once per four steps.  The raw sub-blocks are loaded four steps ahead; the dequant
-//    of step k+1 is spread over the MFMAs of step k, a few VALU ops per MFMA.
+//    once per four steps.  The raw sub-blocks are loaded eight steps ahead (Q8_0: four,
+//    for registers); the dequant of step k+1 is spread over the MFMAs of step k, a few
+//    VALU ops per MFMA.
 //  * One barrier per step, half way through it: the next stage is then complete and the
 //    previous one free for the DMA three steps ahead.
 //  * The MFMAs take the weights as the first operand, so each lane's accumulators hold
@@ -53,7 +54,10 @@ typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 
 constexpr int TN = 256, TK = 64;
 constexpr int NSTAGE = 4;              // activation stages (DMA three steps ahead)
-constexpr int PD = 4;                  // raw weight prefetch distance (steps)
+// Raw weight prefetch distance (steps; a multiple of four): eight where the ring fits
+// the register budget beside the accumulators, four for Q8_0's larger sub-blocks.
+template <int QT>
+constexpr int prefetch_steps() { return QT == QT_Q8_0 ? 4 : 8; }
 
 struct TileParams {
   const void* x;
@@ -181,10 +185,12 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     row_sb[j] = rok[j] ? (uint32_t)n * (uint32_t)nsb : 0u;
   }
 
-  // Ring of raw sub-blocks: step k lives in slot k % PD.  Every index below is static
-  // (the K loop is unrolled by four, PD = 4), so the ring stays in registers.
+  // Ring of raw sub-blocks: step kt0 + k lives in slot k % PD.  Every index below is
+  // static (the K loop is unrolled by PD), so the ring stays in registers.  K-quant
+  // super-block headers ride with the first step of their super-block (slots 0, 4).
+  constexpr int PD = prefetch_steps<QT>();
   Raw<QT> raw[PD][2];
-  Hdr<QT> hdr[2];
+  Hdr<QT> hdr[PD / 4][2];
   Scales<QT> sc[2];
   auto issue_raw = [&](int kt, auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;
@@ -192,24 +198,23 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     const bool in = kt < kend && sb < nsub;
 #pragma unroll
     for (int j = 0; j < 2; ++j) load_raw<QT>(R, row_sub[j], sb, in && rok[j], raw[slot][j]);
-    if constexpr (is_kquant(QT) && slot == 0) {
-      // first step of a super-block (K-quant steps come in whole super-blocks of four)
+    if constexpr (is_kquant(QT) && slot % 4 == 0) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) load_hdr<QT>(R, row_sb[j], kt >> 2, in && rok[j], hdr[j]);
+      for (int j = 0; j < 2; ++j) load_hdr<QT>(R, row_sb[j], kt >> 2, in && rok[j], hdr[slot / 4][j]);
     }
   };
 
   // VMEM instructions issue_raw issues for the step with ring slot s.
   constexpr int RB = 2 * raw_loads<QT>(), RH = 2 * hdr_loads<QT>();  // two weight rows
-  auto rops = [](int slot) constexpr { return RB + (slot == 0 ? RH : 0); };
+  auto rops = [](int slot) constexpr { return RB + (slot % 4 == 0 ? RH : 0); };
   // B fragments of the current step, [j][kk]; word kk is replaced by the next step's
   // right after the MFMAs of slice kk have been issued.
   uint4 bf[2][4];
   auto decode_step = [&](auto SLOT) {
-    constexpr int slot = decltype(SLOT)::value;  // == step % 4 == sub-block quarter
-    if constexpr (is_kquant(QT) && slot == 0) {
+    constexpr int slot = decltype(SLOT)::value;  // step % PD; slot % 4 = sub-block quarter
+    if constexpr (is_kquant(QT) && slot % 4 == 0) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) decode_hdr<QT>(hdr[j], h, sc[j]);
+      for (int j = 0; j < 2; ++j) decode_hdr<QT>(hdr[slot / 4][j], h, sc[j]);
     }
   };
 
@@ -231,27 +236,27 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     return *(const uint4*)(lds + stage * A_STAGE + r * 128 + c * 16);
   };
 
-  // ---- prologue: the issue order of steps -3 .. -1 (DMA of step s+3, raw loads of step
-  // s+4), preceded by the raw loads of step 0, so every wait below is the steady-state one
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  issue_raw(kt0, I0());
+  // ---- prologue.  Steady state issues, in step s: the DMA of stage s+3 half way and the
+  // raw loads of step s+PD at the end.  The prologue issues raw loads of steps
+  // 0 .. PD-3, the DMAs of stages 0 and 1, raw PD-2, DMA 2, raw PD-1: after the DMA of
+  // any stage k, exactly raw(k+PD-2), DMA(k+1), raw(k+PD-1) follow, as in the loop.
+  sfor<PD - 2>([&](auto S_) {
+    constexpr int s_ = decltype(S_)::value;
+    issue_raw(kt0 + s_, std::integral_constant<int, s_>());
+  });
   issue_a(kt0);
-  issue_raw(kt0 + 1, I1());
   issue_a(kt0 + 1);
-  issue_raw(kt0 + 2, I2());
+  issue_raw(kt0 + PD - 2, std::integral_constant<int, PD - 2>());
   issue_a(kt0 + 2);
-  issue_raw(kt0 + 3, I3());
-  decode_step(I0());
+  issue_raw(kt0 + PD - 1, std::integral_constant<int, PD - 1>());
+  decode_step(std::integral_constant<int, 0>());
   sfor<4>([&](auto KK) {
     constexpr int kk = decltype(KK)::value;
 #pragma unroll
     for (int j = 0; j < 2; ++j) bf[j][kk] = dequant_word<QT, XT, kk>(raw[0][j], sc[j], 0, p.nib);
   });
   // stage 0 complete (every wavefront's DMA of it) before its first fragments are read
-  vm_wait<2 * MI + rops(1) + rops(2) + rops(3)>();
+  vm_wait<2 * MI + rops(PD - 2) + rops(PD - 1)>();
   __syncthreads();
   // Activation fragments stream through a ring of four registers, three ahead, across
   // step boundaries.
@@ -271,22 +276,23 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   // goes into it.  The raw weights of step kt+4 are loaded at the end, into the ring
   // slot step kt just used.
   auto step = [&](int kt, auto U) {
-    constexpr int u = decltype(U)::value;
-    constexpr int un = (u + 1) & 3;
+    constexpr int u = decltype(U)::value;      // (kt - kt0) % PD; LDS stage u % 4
+    constexpr int un = (u + 1) % PD;
     using SN = std::integral_constant<int, un>;
     WordTmp<QT> wt[2];
     uint32_t nw[2][4];
     sfor<NSLOT>([&](auto MS) {
       constexpr int m = decltype(MS)::value, f = m >> 1, j = m & 1, kk = f / MI, i = f % MI;
       constexpr int ts = m - kk * SPS;  // slot within the slice
-      if constexpr (j == 0 && f + 3 < NF) ring[(f + 3) & 3] = read_a(u, f + 3);
-      if constexpr (j == 0 && f + 3 >= NF) ring[(f + 3) & 3] = read_a(un, f + 3 - NF);
+      if constexpr (j == 0 && f + 3 < NF) ring[(f + 3) & 3] = read_a(u & 3, f + 3);
+      if constexpr (j == 0 && f + 3 >= NF) ring[(f + 3) & 3] = read_a(un & 3, f + 3 - NF);
       acc[i][j] = mfma<XT>(bf[j][kk], ring[f & 3], acc[i][j]);
       if constexpr (m == 0) decode_step(SN());
       if constexpr (m == NSLOT / 2 - 1) {
         // this wavefront's DMA of stage kt+1 was issued half way through step kt-2;
-        // after it: the raw loads of kt+2, the DMA of stage kt+2, the raw loads of kt+3
-        vm_wait<MI + rops((u + 2) & 3) + rops((u + 3) & 3)>();
+        // after it: the raw loads of kt+PD-2, the DMA of stage kt+2, the raw loads of
+        // kt+PD-1
+        vm_wait<MI + rops((u + PD - 2) % PD) + rops((u + PD - 1) % PD)>();
         __syncthreads();
         issue_a(kt + NSTAGE - 1);
       }
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
         constexpr int k = decltype(TK_)::value;
         if constexpr ((k * SPS) / 10 == ts) {
           constexpr int jw = k / 5, kq = k % 5;
-          if constexpr (kq == 0) word_prelude<QT, kk>(raw[un][jw], sc[jw], un, p.nib, wt[jw]);
+          if constexpr (kq == 0) word_prelude<QT, kk>(raw[un][jw], sc[jw], un & 3, p.nib, wt[jw]);
           else nw[jw][kq - 1] = word_quarter<QT, XT, kk, kq - 1>(wt[jw], p.nib);
         }
       });
@@ -309,11 +315,12 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     issue_raw(kt + PD, U);
   };
 
-  for (int kt = kt0; kt < kend; kt += 4) {
-    step(kt, I0());
-    if (kt + 1 < kend) step(kt + 1, I1());
-    if (kt + 2 < kend) step(kt + 2, I2());
-    if (kt + 3 < kend) step(kt + 3, I3());
+  for (int kt = kt0; kt < kend; kt += PD) {
+    step(kt, std::integral_constant<int, 0>());
+    sfor<PD - 1>([&](auto U_) {
+      constexpr int u = decltype(U_)::value + 1;
+      if (kt + u < kend) step(kt + u, std::integral_constant<int, u>());
+    });
   }
 
   // no DMA may still be landing in LDS when the workgroup ends
