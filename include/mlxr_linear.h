@@ -1,0 +1,72 @@
+// Quantized Linear and MLP layers over the q_gemm_dequant operator: the caller side of the
+// path, as the reference plans it for core/graph/layers.cpp:86-99 (Linear::forward,
+// y = x W^T + b over x [..., in_features]) with M = batch * seq
+// (docs/SESSION_2025_11_07_MODEL_LOADING.md:133-160), and MLP::forward
+// (layers.cpp:391-414: down(swish(gate(x)) * up(x))).
+//
+// Names and meaning follow the reference classes (core/graph/layers.h:59-94 Linear; MLP
+// beside it); the weight is held as packed GGUF blocks in device memory instead of an MLX
+// float tensor.  forward() takes and returns device arrays (bf16 or fp16 activations,
+// output in the input dtype) and runs on the given HIP stream; it is stream-ordered and
+// allocates only its output (plus a split-K workspace the first time a large M needs one,
+// kept by the layer).  One layer must not run forward on two streams at once (the
+// workspace is per layer).  Errors throw std::runtime_error, as the reference does.
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "mlxr_gguf.h"
+#include "q_gemm_dequant_primitive.h"
+
+namespace mlxr {
+namespace graph {
+
+class Linear {
+ public:
+  // in_features = K, out_features = N (reference layers.h:67).
+  Linear(int in_features, int out_features, bool bias = false);
+
+  // Weight [out_features, in_features] as GGUF blocks in host memory (e.g. a mapped
+  // tensor), packed into device memory once.
+  void load_weight(const void* gguf_host, kernels::QuantType quant_type, kernels::Stream s = {});
+  // Weight tensor `name` of an open GGUF file (ggml dims {in_features, out_features}).
+  void load_weight(const mlxr_gguf* file, const std::string& name, kernels::Stream s = {});
+  // Bias [out_features] on the device (fp32, fp16 or bf16).  Only for layers built with bias.
+  void set_bias(const kernels::array& bias);
+
+  // x [..., in_features] -> [..., out_features], M = product of the leading dims.
+  kernels::array forward(const kernels::array& x, kernels::Stream s = {});
+
+  const kernels::array& weight() const { return weight_; }
+  const kernels::array* bias() const { return has_bias_ ? &bias_ : nullptr; }
+  int in_features() const { return in_features_; }
+  int out_features() const { return out_features_; }
+
+ private:
+  friend class MLP;
+  void run(const kernels::array& x, int M, kernels::array& y, kernels::Stream s);
+  int in_features_, out_features_;
+  bool has_bias_;
+  kernels::array weight_;  // Dtype::packed
+  kernels::array bias_;
+  kernels::array workspace_;  // split-K partial sums, grown on demand
+};
+
+// SwiGLU MLP (reference layers.cpp:383-414): down(swish(gate(x)) * up(x)).  gate and up
+// read the same x and run as one grouped call (one launch for M <= 4).
+class MLP {
+ public:
+  MLP(int hidden_size, int intermediate_size);
+  Linear& gate_proj() { return gate_; }
+  Linear& up_proj() { return up_; }
+  Linear& down_proj() { return down_; }
+  kernels::array forward(const kernels::array& x, kernels::Stream s = {});
+
+ private:
+  int hidden_, inter_;
+  Linear gate_, up_, down_;
+};
+
+}  // namespace graph
+}  // namespace mlxr

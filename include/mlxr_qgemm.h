@@ -158,6 +158,12 @@ typedef struct mlxr_qgemm_item {
 int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
                            void* stream);
 
+/* out[i] = swish(gate[i]) * up[i], swish(g) = g / (1 + exp(-g)), computed in fp32 and
+ * rounded to dtype (MLXR_F32 / MLXR_F16 / MLXR_BF16); out may alias gate or up.  The
+ * gating of the SwiGLU MLP between its gate/up and down projections (reference
+ * core/graph/layers.cpp:391-414, MLP::forward). */
+int mlxr_swiglu(const void* gate_dev, const void* up_dev, void* out_dev, size_t n, int dtype, void* stream);
+
 /* Deterministic synthetic inputs with the shapes/distributions of the benchmark
  * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by
  * Box-Muller in double precision.

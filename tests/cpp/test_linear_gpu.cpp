@@ -1,0 +1,115 @@
+// C++ Linear / MLP layers (include/mlxr_linear.h) on the GPU: Linear::forward over a 3-D
+// input equals the q_gemm_dequant operator on the flattened rows bit for bit (same kernel
+// at these M), a GGUF-loaded weight gives the same result as one packed from host bytes,
+// and MLP::forward equals the chain gate/up -> mlxr_swiglu -> down.  Built and run by
+// tests/test_layers.py (GPU); prints "OK <n>" on success.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "mlxr_gguf.h"
+#include "mlxr_linear.h"
+#include "mlxr_qgemm.h"
+
+using namespace mlxr;
+using kernels::array;
+using kernels::Dtype;
+using kernels::QuantType;
+
+static int checks = 0;
+#define EXPECT(c)                                             \
+  do {                                                        \
+    ++checks;                                                 \
+    if (!(c)) {                                               \
+      std::printf("FAIL %s:%d %s\n", __FILE__, __LINE__, #c); \
+      return 1;                                               \
+    }                                                         \
+  } while (0)
+
+static std::vector<uint8_t> to_host(const array& a) {
+  std::vector<uint8_t> h(a.nbytes());
+  if (hipMemcpy(h.data(), a.data<void>(), a.nbytes(), hipMemcpyDeviceToHost) != hipSuccess)
+    throw std::runtime_error("copy");
+  return h;
+}
+
+static array act(int rows, int K, uint64_t seed) {
+  std::vector<uint16_t> h((size_t)rows * K);
+  mlxr_synth_act(h.size(), MLXR_BF16, seed, h.data());
+  array a({rows, K}, Dtype::bfloat16);
+  if (hipMemcpy(a.data<void>(), h.data(), h.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+    throw std::runtime_error("copy");
+  return a;
+}
+
+int main(int argc, char** argv) {
+  const char* gguf_path = argc > 1 ? argv[1] : nullptr;  // file with tensor "w" (Q4_K, dims {512, 384})
+  const int K = 512, N = 384;
+  std::vector<uint8_t> w((size_t)N * K / 256 * 144);
+  mlxr_synth_gguf(MLXR_Q4_K, N, K, 77, w.data());
+
+  graph::Linear lin(K, N, true);
+  lin.load_weight(w.data(), QuantType::Q4_K);
+  std::vector<uint16_t> bh(N);
+  mlxr_synth_act(N, MLXR_BF16, 5, bh.data());
+  array bias({N}, Dtype::bfloat16);
+  hipMemcpy(bias.data<void>(), bh.data(), N * 2, hipMemcpyHostToDevice);
+  lin.set_bias(bias);
+
+  for (int M : {1, 3, 40}) {
+    array x2 = act(M, K, 100 + M);
+    array x3 = array::borrow(x2.data<void>(), {1, M, K}, Dtype::bfloat16);
+    array y3 = lin.forward(x3);
+    EXPECT(y3.ndim() == 3 && y3.shape(0) == 1 && y3.shape(1) == M && y3.shape(2) == N);
+    array yo = kernels::q_gemm_dequant(x2, lin.weight(), M, N, K, QuantType::Q4_K, 0, &bias);
+    hipDeviceSynchronize();
+    EXPECT(to_host(y3) == to_host(yo));
+  }
+
+  if (gguf_path) {
+    mlxr_gguf* g = nullptr;
+    EXPECT(mlxr_gguf_open(gguf_path, &g) == 0);
+    graph::Linear lg(K, N, true);
+    lg.load_weight(g, "w");
+    lg.set_bias(bias);
+    array x = act(7, K, 9);
+    array a = lg.forward(x), b = lin.forward(x);
+    hipDeviceSynchronize();
+    EXPECT(to_host(a) == to_host(b));
+    bool threw = false;
+    try {
+      lg.load_weight(g, "missing");
+    } catch (const std::runtime_error&) {
+      threw = true;
+    }
+    EXPECT(threw);
+    mlxr_gguf_close(g);
+  }
+
+  // MLP: hidden 256, intermediate 512
+  const int H = 256, I = 512;
+  graph::MLP mlp(H, I);
+  std::vector<uint8_t> wg((size_t)I * H / 256 * 144), wu(wg.size()), wd((size_t)H * I / 256 * 144);
+  mlxr_synth_gguf(MLXR_Q4_K, I, H, 1, wg.data());
+  mlxr_synth_gguf(MLXR_Q4_K, I, H, 2, wu.data());
+  mlxr_synth_gguf(MLXR_Q4_K, H, I, 3, wd.data());
+  mlp.gate_proj().load_weight(wg.data(), QuantType::Q4_K);
+  mlp.up_proj().load_weight(wu.data(), QuantType::Q4_K);
+  mlp.down_proj().load_weight(wd.data(), QuantType::Q4_K);
+  for (int M : {2, 24}) {
+    array x = act(M, H, 50 + M);
+    array y = mlp.forward(x);
+    array g = mlp.gate_proj().forward(x), u = mlp.up_proj().forward(x);
+    array h({M, I}, Dtype::bfloat16);
+    EXPECT(mlxr_swiglu(g.data<void>(), u.data<void>(), h.data<void>(), (size_t)M * I, MLXR_BF16, nullptr) == 0);
+    array y2 = mlp.down_proj().forward(h);
+    hipDeviceSynchronize();
+    EXPECT(to_host(y) == to_host(y2));
+  }
+  std::printf("OK %d\n", checks);
+  return 0;
+}
