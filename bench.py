@@ -16,6 +16,7 @@ The other BASELINE configurations are reported under "configs":
 launch overhead is not in their figures.)
   c4  Q4_K prefill GEMM, Llama-3-8B set, M in {512, 2048} (bf16 MFMA)
   c5  Llama-3-70B layer, Q4_K + Q6_K (v, down), 7 GEMMs in a hipGraph at M=1 and M=256
+  mlp (extra) Llama-3-8B gate/up + SwiGLU gating at M=1, fused vs grouped + gating kernel
 The CPU baseline is the reference's CPU path (dequantize all of W to fp32, then the naive
 fp32 loop; restated in oracle/orc.c) on the headline workload, one thread.
 
@@ -51,7 +52,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="headline,c1,c3,c4,c5")
+    ap.add_argument("--only", default="headline,c1,c3,c4,c5,mlp")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--skip-dropin", action="store_true",
                     help="do not time the seven-call drop-in step (profiler runs of the headline kernel)")
@@ -309,6 +310,32 @@ def run_c4(cx, args):
     return res
 
 
+def run_mlp(cx, args):
+    """Llama-3-8B MLP gate/up half at M = 1: fused gate + up + gating (one launch) against the
+    grouped gate/up launch followed by the gating kernel.  Not a BASELINE config."""
+    mx, torch = cx.mx, cx.torch
+    specs = [(n, N, K, Q4K) for n, N, K in LLAMA3_8B if n in ("gate", "up")]
+    _, copies, _ = pack_copies(cx, specs, SEED_BASE + 6)
+    x = cx.act(1, 4096, mx.BF16, SEED_BASE + 6001)
+    h = torch.empty((1, 14336), dtype=torch.bfloat16, device=cx.dev)
+    g = torch.empty_like(h)
+    u = torch.empty_like(h)
+    fused = lambda r: mx.q_gemm_swiglu(x, copies[r % len(copies)]["gate"], copies[r % len(copies)]["up"], out=h)
+
+    def unfused(r):
+        W = copies[r % len(copies)]
+        mx.q_gemm_dequant_grouped(x, [W["gate"], W["up"]], outs=[g, u])
+        mx.swiglu(g, u, out=h)
+
+    b = 2 * mx.gguf_size(Q4K, 14336, 4096) + 4096 * 2 + 14336 * 2
+    res = {}
+    for name, fn in (("fused", fused), ("grouped_plus_gating", unfused)):
+        fn(0)
+        us = 1e3 * cx.graph_ms(fn, 2 * len(copies))
+        res[name] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+    return res
+
+
 def run_c5(cx, args):
     mx, torch = cx.mx, cx.torch
     _, copies, layer = pack_copies(cx, LLAMA3_70B, SEED_BASE + 4, min_copies=2)
@@ -362,7 +389,7 @@ def main():
         run_headline(cx, args, out)
     configs = {}
     for key, fn in (("c1_q8_0_gemv_tinyllama", run_c1), ("c3_q4k_skinny", run_c3), ("c4_q4k_prefill", run_c4),
-                    ("c5_llama3_70b_layer_graph", run_c5)):
+                    ("c5_llama3_70b_layer_graph", run_c5), ("mlp_swiglu_m1", run_mlp)):
         if key.split("_")[0] in only:
             configs[key] = fn(cx, args)
             torch.cuda.empty_cache()

@@ -53,8 +53,8 @@ class Linear {
   kernels::array workspace_;  // split-K partial sums, grown on demand
 };
 
-// SwiGLU MLP (reference layers.cpp:383-414): down(swish(gate(x)) * up(x)).  gate and up
-// read the same x and run as one grouped call (one launch for M <= 4).
+// SwiGLU MLP (reference layers.cpp:383-414): down(swish(gate(x)) * up(x)).  gate, up and
+// the gating run as mlxr_qgemm_swiglu: one launch for M <= 4.
 class MLP {
  public:
   MLP(int hidden_size, int intermediate_size);

@@ -158,6 +158,18 @@ typedef struct mlxr_qgemm_item {
 int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
                            void* stream);
 
+/* h[M, N] = swish(X . Wg^T) * (X . Wu^T): the gate/up half of a SwiGLU MLP
+ * (reference core/graph/layers.cpp:391-414; swiglu_mlp_fused.metal:131-345 plans the
+ * fusion).  gate_packed and up_packed are packed weights of the same type and [N, K].
+ * At M <= 4 one launch computes both projections and the gating (no gate/up outputs ever
+ * reach memory) and needs no workspace; above, it runs the two projections and
+ * mlxr_swiglu, and the up projection goes to the caller's workspace of
+ * mlxr_qgemm_swiglu_workspace_size bytes.  No counterpart in the reference's operator. */
+int mlxr_qgemm_swiglu_workspace_size(int qtype, int N, int K, int M, int h_dtype, size_t* bytes);
+int mlxr_qgemm_swiglu(int qtype, int N, int K, const void* gate_packed, const void* up_packed,
+                      const void* x_dev, int x_dtype, void* h_dev, int h_dtype, int M,
+                      void* workspace_dev, size_t workspace_bytes, void* stream);
+
 /* out[i] = swish(gate[i]) * up[i], swish(g) = g / (1 + exp(-g)), computed in fp32 and
  * rounded to dtype (MLXR_F32 / MLXR_F16 / MLXR_BF16); out may alias gate or up.  The
  * gating of the SwiGLU MLP between its gate/up and down projections (reference

@@ -110,26 +110,22 @@ kernels::array MLP::forward(const kernels::array& x, kernels::Stream s) {
   for (int d = 0; d + 1 < x.ndim(); ++d) M *= x.shape(d);
   std::vector<int> hshape = x.shape();
   hshape.back() = inter_;
-  kernels::array g(hshape, x.dtype()), u(hshape, x.dtype());
+  kernels::array g(hshape, x.dtype());
   if (M > 0) {
-    if (M <= 4) {
-      // gate and up read the same x: one grouped call (a single launch at M <= 4)
-      const int ydt = dt_code(x.dtype());
-      mlxr_qgemm_item it[2] = {
-          {(int)gate_.weight_.quant_type(), inter_, hidden_, 0, gate_.weight_.data<void>(), nullptr, MLXR_F32,
-           g.data<void>(), ydt},
-          {(int)up_.weight_.quant_type(), inter_, hidden_, 0, up_.weight_.data<void>(), nullptr, MLXR_F32,
-           u.data<void>(), ydt}};
-      check(mlxr_qgemm_run_grouped(2, it, x.data<void>(), ydt, (int)M, s.hip_stream));
-    } else {
-      gate_.run(x, (int)M, g, s);
-      up_.run(x, (int)M, u, s);
-    }
-    check(mlxr_swiglu(g.data<void>(), u.data<void>(), g.data<void>(), (size_t)M * (size_t)inter_,
-                      dt_code(x.dtype()), s.hip_stream));
+    const int qt = (int)gate_.weight_.quant_type();
+    if (qt != (int)up_.weight_.quant_type()) throw std::runtime_error("MLP: gate and up must share a quant type");
+    const int dt = dt_code(x.dtype());
+    size_t ws = 0;
+    check(mlxr_qgemm_swiglu_workspace_size(qt, inter_, hidden_, (int)M, dt, &ws));
+    kernels::array u;
+    if (ws) u = kernels::array({(int)ws}, kernels::Dtype::uint8);
+    // M <= 4: gate, up and the gating in one launch; above, up goes to u
+    check(mlxr_qgemm_swiglu(qt, inter_, hidden_, gate_.weight_.data<void>(), up_.weight_.data<void>(),
+                            x.data<void>(), dt, g.data<void>(), dt, (int)M, ws ? u.data<void>() : nullptr, ws,
+                            s.hip_stream));
   }
   kernels::array y = down_.forward(g, s);
-  // g and u are freed here (hipFree waits for the device), after the queued kernels
+  // the temporaries are freed here (hipFree waits for the device), after the queued kernels
   return y;
 }
 

@@ -264,6 +264,61 @@ int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* 
   return MLXR_OK;
 }
 
+int mlxr_qgemm_swiglu_workspace_size(int qtype, int N, int K, int M, int h_dtype, size_t* bytes) {
+  mlxr::PackedLayout L;
+  const int rc = check_type_shape(qtype, N, K, &L);
+  if (rc) return rc;
+  if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
+  if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
+  if (!valid_dtype(h_dtype)) return fail(MLXR_E_INVALID, "invalid output dtype %d", h_dtype);
+  mlxr::RunArgs a;
+  a.L = L;
+  a.M = M;
+  *bytes = (M <= kGemvMaxM && mlxr::gemv_groupable(a)) ? 0 : (size_t)M * (size_t)N * (h_dtype == MLXR_F32 ? 4 : 2);
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_swiglu(int qtype, int N, int K, const void* gate_packed, const void* up_packed, const void* x_dev,
+                      int x_dtype, void* h_dev, int h_dtype, int M, void* workspace_dev, size_t workspace_bytes,
+                      void* stream) {
+  size_t need = 0;
+  int rc = mlxr_qgemm_swiglu_workspace_size(qtype, N, K, M, h_dtype, &need);
+  if (rc) return rc;
+  if (x_dtype != MLXR_BF16 && x_dtype != MLXR_F16)
+    return fail(MLXR_E_INVALID, "activation dtype must be BF16 or F16 (got %d)", x_dtype);
+  if (M == 0) return MLXR_OK;
+  if (!gate_packed || !up_packed || !x_dev || !h_dev) return fail(MLXR_E_INVALID, "null buffer");
+  if (need == 0) {
+    mlxr::RunArgs g, u;
+    mlxr::make_layout(qtype, N, K, &g.L);
+    u.L = g.L;
+    g.packed = (const uint8_t*)gate_packed;
+    u.packed = (const uint8_t*)up_packed;
+    g.x = u.x = x_dev;
+    g.x_dtype = u.x_dtype = x_dtype;
+    g.bias = u.bias = nullptr;
+    g.bias_dtype = u.bias_dtype = MLXR_F32;
+    g.y = h_dev;
+    u.y = nullptr;
+    g.y_dtype = u.y_dtype = h_dtype;
+    g.M = u.M = M;
+    const hipError_t e = mlxr::launch_gemv_swiglu(g, u, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "swiglu gemv launch");
+    return MLXR_OK;
+  }
+  // larger M: gate into h, up into the workspace, then the gating in place
+  if (!workspace_dev || workspace_bytes < need)
+    return fail(MLXR_E_INVALID, "swiglu at M=%d needs a workspace of %zu bytes (got %zu)", M, need,
+                workspace_bytes);
+  rc = mlxr_qgemm_run_ex(qtype, N, K, 0, gate_packed, x_dev, x_dtype, nullptr, MLXR_F32, h_dev, h_dtype, M,
+                         MLXR_PATH_AUTO, stream);
+  if (rc) return rc;
+  rc = mlxr_qgemm_run_ex(qtype, N, K, 0, up_packed, x_dev, x_dtype, nullptr, MLXR_F32, workspace_dev, h_dtype, M,
+                         MLXR_PATH_AUTO, stream);
+  if (rc) return rc;
+  return mlxr_swiglu(h_dev, workspace_dev, h_dev, (size_t)M * (size_t)N, h_dtype, stream);
+}
+
 int mlxr_qgemm_run(int qtype, int N, int K, int group_size, const void* packed_dev, const void* x_dev,
                    int x_dtype, const void* bias_dev, int bias_dtype, void* y_dev, int y_dtype, int M,
                    void* stream) {

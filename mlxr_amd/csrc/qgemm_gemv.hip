@@ -18,6 +18,8 @@
 // lane's 32 activations are loaded once per segment and reused for all R rows.
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "qgemm_device.h"
 #include "qgemm_internal.h"
 
@@ -379,6 +381,9 @@ __global__ __launch_bounds__(256) void qgemv_kernel(GemvParams p) {
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr uint32_t OOB = 0x80000000u;  // voffset that is out of range of every buffer
 
+// swish(g) * u = g / (1 + exp(-g)) * u in fp32 (the MLP gating, layers.cpp:391-414).
+__device__ __forceinline__ float swiglu1(float g, float u) { return g / (1.f + __expf(-g)) * u; }
+
 __device__ __forceinline__ rsrc_t make_rsrc(const void* ptr, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)bytes, 0x00020000);
 }
@@ -512,7 +517,10 @@ __device__ __forceinline__ void decode_chunk(const CLoad<QT>& b, int j, uint32_t
   }
 }
 
-template <int QT, int XT, int MT, int D, bool LIN>
+// SW (SwiGLU): the launch has two weights of the same shape, gate (group 0) and up (group
+// 1); a wavefront walks its gate rows, then the same up rows, and stores swish(gate) * up
+// for those rows into group 0's output.
+template <int QT, int XT, int MT, int D, bool LIN, bool SW>
 __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
@@ -550,13 +558,19 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   const int rpw = G.rows_per_wave;
   const int r0 = (gw - G.wave_start) * rpw;
   const int r1 = min(r0 + rpw, N);
-  const int C = r1 > r0 ? (r1 - r0) * nseg : 0;
+  constexpr int NW = SW ? 2 : 1;  // weights walked per row
+  const int C = r1 > r0 ? (r1 - r0) * nseg * NW : 0;
   uint4* xs = (uint4*)smem;                                          // [MT][nseg][4][64]
   float2* Xs = (float2*)(smem + (size_t)MT * nseg * 4096);           // [MT][nseg][64]
 
-  rsrc_t R[4];
+  rsrc_t R[4], RU[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) R[i] = make_rsrc(G.P.p[i] ? G.P.p[i] : (const uint8_t*)lp.x, G.psize[i]);
+  if constexpr (SW) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      RU[i] = make_rsrc(lp.g[1].P.p[i] ? lp.g[1].P.p[i] : (const uint8_t*)lp.x, lp.g[1].psize[i]);
+  }
 
   // Activation loads go out first (two padded tasks per thread; padding reads zeros),
   // then the weight prefetch, so the in-order memory counter never makes the LDS staging
@@ -580,9 +594,23 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   if (T > 256) xload(threadIdx.x + 256, xc);
 
   CLoad<QT> buf[D];
+  // SW: a wavefront walks all its gate rows, then the same up rows (chunk c < CG: gate)
+  const int CG = SW ? C / 2 : C;
   auto issue = [&](int c, CLoad<QT>& b) {
-    const int cc = max(min(c, C - 1), 0);
-    if constexpr (LIN) {
+    int cc = max(min(c, C - 1), 0);
+    if constexpr (SW) {
+      const bool up = cc >= CG;
+      cc = up ? cc - CG : cc;
+      rsrc_t Rs[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Rs[i] = up ? RU[i] : R[i];
+      if constexpr (LIN) {
+        load_chunk<QT>(Rs, r0, cc, nsub, nsb, lane, true, b);
+      } else {
+        const int rl = cc / nseg, seg = cc - rl * nseg;
+        load_chunk<QT>(Rs, min(r0 + rl, N - 1), seg, nsub, nsb, lane, seg * 64 + lane < nsub, b);
+      }
+    } else if constexpr (LIN) {
       // every row is exactly nseg full segments: chunk cc starts at sub-block r0*nsub + 64*cc
       load_chunk<QT>(R, r0, cc, nsub, nsb, lane, true, b);
     } else {
@@ -624,10 +652,10 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = 0.f;
-  float res = 0.f;
+  float res = 0.f, res_up = 0.f;
   const uint32_t MASK = lp.cmask, MAGIC = lp.cmagic;
 
-  auto compute = [&](const CLoad<QT>& b, const int rl, const int seg) {
+  auto compute = [&](const CLoad<QT>& b, const int rl, const int seg, const bool up) {
     WDec wd;
     decode_chunk<QT, XT>(b, lane & 7, MASK, MAGIC, wd);
 #pragma unroll
@@ -653,7 +681,8 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
       for (int m = 0; m < MT; ++m) {
         if (m < M) {
           const float tot = wave_total(acc[m]);
-          res = (lane == rl * MT + m) ? tot : res;
+          if (SW && up) res_up = (lane == rl * MT + m) ? tot : res_up;
+          else res = (lane == rl * MT + m) ? tot : res;
         }
         acc[m] = 0.f;
       }
@@ -662,26 +691,32 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
 
   // Steady state: D chunks per trip, every load and compute unconditional.
   // (row_local, segment) of the chunk being reduced: uniform loop state.
+  // (SW: which weight of the row pair, also uniform)
   int c = 0, rl = 0, seg = 0;
+  bool up = false;
+  auto advance = [&]() {
+    if (++seg == nseg) {
+      seg = 0;
+      ++rl;
+      if (SW && !up && rl == r1 - r0) {
+        rl = 0;
+        up = true;
+      }
+    }
+  };
   for (; c + D <= C; c += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       issue(c + d + D - 1, buf[(d + D - 1) % D]);
-      compute(buf[d], rl, seg);
-      if (++seg == nseg) {
-        seg = 0;
-        ++rl;
-      }
+      compute(buf[d], rl, seg, up);
+      advance();
     }
   }
 #pragma unroll
   for (int d = 0; d < D - 1; ++d) {
     if (c + d < C) {
-      compute(buf[d], rl, seg);
-      if (++seg == nseg) {
-        seg = 0;
-        ++rl;
-      }
+      compute(buf[d], rl, seg, up);
+      advance();
     }
   }
 
@@ -690,6 +725,11 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   if (orl < r1 - r0 && om < M) {
     float v = res;
     if (G.bias) v += load_scalar(G.bias, G.bias_dtype, (size_t)(r0 + orl));
+    if constexpr (SW) {
+      float u = res_up;
+      if (lp.g[1].bias) u += load_scalar(lp.g[1].bias, lp.g[1].bias_dtype, (size_t)(r0 + orl));
+      v = swiglu1(v, u);
+    }
     store_scalar(G.y, G.y_dtype, (size_t)om * N + r0 + orl, v);
   }
 }
@@ -725,12 +765,16 @@ int env_int(const char* name, int dflt) {
   return e ? atoi(e) : dflt;
 }
 
-template <int QT, int XT, int MT, int D>
+template <int QT, int XT, int MT, int D, bool SW = false>
 hipError_t launch_lds_t(const LdsParams& lp, unsigned grid, hipStream_t s) {
-  if (((lp.K >> 5) & 63) == 0)
-    qgemv_lds_kernel<QT, XT, MT, D, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
+  if (SW && ((lp.K >> 5) & 63) == 0)
+    qgemv_lds_kernel<QT, XT, MT, D, true, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
+  else if (SW)
+    qgemv_lds_kernel<QT, XT, MT, D, false, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
+  else if (((lp.K >> 5) & 63) == 0)
+    qgemv_lds_kernel<QT, XT, MT, D, true, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
   else
-    qgemv_lds_kernel<QT, XT, MT, D, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
+    qgemv_lds_kernel<QT, XT, MT, D, false, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
   return hipGetLastError();
 }
 
@@ -851,6 +895,27 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s) {
 
 bool gemv_groupable(const RunArgs& a) { return a.M <= 4 && lds_fits(a.M, a.L.K, a.L, mt_for(a.M)); }
 
+template <int QT, int XT>
+hipError_t launch_lds_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t s) {
+  static const int depth = env_int("MLXR_GEMV_DEPTH", 3);
+  const RunArgs* items[2] = {&gate, &up};
+  LdsParams lp;
+  lds_setup(items, 2, lp);
+  // every wavefront works on gate rows (and the same up rows): group 1 owns no wavefronts;
+  // as many wavefronts as a grouped launch of the two weights would have
+  const long target = (long)num_cus() * waves_per_cu_target();
+  lp.g[0].rows_per_wave = lp.g[1].rows_per_wave =
+      (int)std::min<long>(64 / mt_for(gate.M), std::max<long>(1, (gate.L.N + target - 1) / target));
+  lp.g[1].wave_start = 0x7fffffff;
+  const int waves = (gate.L.N + lp.g[0].rows_per_wave - 1) / lp.g[0].rows_per_wave;
+  const unsigned grid = (unsigned)((waves + 3) / 4);
+  const int M = lp.M;
+  (void)depth;
+  if (M == 1) return launch_lds_t<QT, XT, 1, 3, true>(lp, grid, s);
+  if (M == 2) return launch_lds_t<QT, XT, 2, 3, true>(lp, grid, s);
+  return launch_lds_t<QT, XT, 4, 3, true>(lp, grid, s);
+}
+
 hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s) {
   const RunArgs& a = *items[0];
   const bool f16 = a.x_dtype == DT_F16;
@@ -860,6 +925,17 @@ hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s
     case QT_Q4_0: return f16 ? launch_lds<QT_Q4_0, X_F16>(items, n, s) : launch_lds<QT_Q4_0, X_BF16>(items, n, s);
     case QT_Q4_1: return f16 ? launch_lds<QT_Q4_1, X_F16>(items, n, s) : launch_lds<QT_Q4_1, X_BF16>(items, n, s);
     default: return f16 ? launch_lds<QT_Q8_0, X_F16>(items, n, s) : launch_lds<QT_Q8_0, X_BF16>(items, n, s);
+  }
+}
+
+hipError_t launch_gemv_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t s) {
+  const bool f16 = gate.x_dtype == DT_F16;
+  switch (gate.L.qtype) {
+    case QT_Q4_K: return f16 ? launch_lds_swiglu<QT_Q4_K, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q4_K, X_BF16>(gate, up, s);
+    case QT_Q6_K: return f16 ? launch_lds_swiglu<QT_Q6_K, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q6_K, X_BF16>(gate, up, s);
+    case QT_Q4_0: return f16 ? launch_lds_swiglu<QT_Q4_0, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q4_0, X_BF16>(gate, up, s);
+    case QT_Q4_1: return f16 ? launch_lds_swiglu<QT_Q4_1, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q4_1, X_BF16>(gate, up, s);
+    default: return f16 ? launch_lds_swiglu<QT_Q8_0, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q8_0, X_BF16>(gate, up, s);
   }
 }
 

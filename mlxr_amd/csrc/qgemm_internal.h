@@ -46,6 +46,9 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s);
 // gemv_groupable() tells whether an item qualifies.  n <= 4.
 bool gemv_groupable(const RunArgs& a);
 hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s);
+// gate and up (same type and shape, both groupable) in one launch storing
+// swish(x.gate^T) * (x.up^T) into gate.y.
+hipError_t launch_gemv_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t s);
 
 // MFMA GEMM (qgemm_tile.hip).  Any M >= 1 (rows beyond M are masked).  With a.ws, shapes
 // with too few tiles for the device split K over workgroups (fp32 partials in a.ws).

@@ -6,8 +6,6 @@ x [..., in_features] with M = batch * seq, layers.cpp:86-99) and MLP::forward
 (layers.cpp:391-414: down(swish(gate(x)) * up(x))).  Weights are packed GGUF blocks on the
 device; every computation runs in libmlxr_qgemm.so (torch supplies memory and streams).
 """
-import ctypes
-
 from . import qgemm
 from .qgemm import BF16, F16, F32, PackedWeight, QGemmError
 
@@ -23,11 +21,7 @@ def swiglu(gate, up, out=None, stream=None):
         raise QGemmError(-3, "gate and up must have the same shape and dtype")
     gate, up = gate.contiguous(), up.contiguous()
     out = torch.empty_like(gate) if out is None else out
-    lib = qgemm.lib()
-    f = lib.mlxr_swiglu
-    f.restype = ctypes.c_int
-    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
-    qgemm._check(f(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(), _dt(torch, gate.dtype),
+    qgemm._check(qgemm.lib().mlxr_swiglu(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(), _dt(torch, gate.dtype),
                    qgemm._stream_ptr(stream)))
     return out
 
@@ -89,7 +83,7 @@ class Linear:
 
 
 class MLP:
-    """down(swish(gate(x)) * up(x)); gate and up run as one grouped call."""
+    """down(swish(gate(x)) * up(x)); at M <= 4 gate, up and the gating are one launch."""
 
     def __init__(self, hidden_size, intermediate_size):
         self.hidden_size, self.intermediate_size = hidden_size, intermediate_size
@@ -103,12 +97,13 @@ class MLP:
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.hidden_size)
         M = x2.shape[0]
-        if M <= 4:
-            g, u = qgemm.q_gemm_dequant_grouped(x2, [self.gate_proj.weight, self.up_proj.weight], stream=stream)
+        gw, uw = self.gate_proj.weight, self.up_proj.weight
+        if M <= 4 and (gw.qtype, gw.N) == (uw.qtype, uw.N):
+            h = qgemm.q_gemm_swiglu(x2, gw, uw, stream=stream)  # one fused launch
         else:
             g = self.gate_proj.forward(x2, stream=stream)
             u = self.up_proj.forward(x2, stream=stream)
-        h = swiglu(g, u, out=g, stream=stream)
+            h = swiglu(g, u, out=g, stream=stream)
         return self.down_proj.forward(h, stream=stream).reshape(*lead, self.hidden_size)
 
     __call__ = forward

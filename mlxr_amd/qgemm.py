@@ -70,6 +70,9 @@ _SIGS = {
     "mlxr_qgemm_run_ex": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_workspace_size": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_size_t)]),
     "mlxr_qgemm_run_ws": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mlxr_qgemm_swiglu_workspace_size": (ctypes.c_int, [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_size_t)]),
+    "mlxr_qgemm_swiglu": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mlxr_swiglu": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run_grouped": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
@@ -273,3 +276,27 @@ def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=Non
                       _dt_code(b.dtype) if b is not None else F32, y.data_ptr(), _dt_code(y.dtype))
     _check(lib().mlxr_qgemm_run_grouped(n, arr, input.data_ptr(), _dt_code(input.dtype), M, _stream_ptr(stream)))
     return outs
+
+
+def q_gemm_swiglu(input, gate, up, out=None, out_dtype=None, stream=None):
+    """h = swish(input . gate^T) * (input . up^T) for packed gate/up weights of one shape
+    (mlxr_qgemm_swiglu: a single fused launch at M <= 4)."""
+    torch = _torch()
+    M, K = input.shape
+    if (gate.qtype, gate.N, gate.K) != (up.qtype, up.N, up.K) or gate.K != K:
+        raise QGemmError(-3, "gate and up must be packed weights of the same type and [N, K]")
+    if not input.is_contiguous():
+        input = input.contiguous()
+    if out is None:
+        out = torch.empty((M, gate.N), dtype=out_dtype or input.dtype, device=input.device)
+    n = ctypes.c_size_t(0)
+    _check(lib().mlxr_qgemm_swiglu_workspace_size(int(gate.qtype), gate.N, K, M, _dt_code(out.dtype), ctypes.byref(n)))
+    ws = None
+    if n.value:
+        with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+            ws = torch.empty(n.value, dtype=torch.uint8, device=input.device)
+    _check(lib().mlxr_qgemm_swiglu(int(gate.qtype), gate.N, K, gate.data_ptr(), up.data_ptr(), input.data_ptr(),
+                                   _dt_code(input.dtype), out.data_ptr(), _dt_code(out.dtype), M,
+                                   ws.data_ptr() if ws is not None else None, n.value, _stream_ptr(stream)))
+    return out
+

@@ -1,7 +1,8 @@
 // C++ Linear / MLP layers (include/mlxr_linear.h) on the GPU: Linear::forward over a 3-D
 // input equals the q_gemm_dequant operator on the flattened rows bit for bit (same kernel
 // at these M), a GGUF-loaded weight gives the same result as one packed from host bytes,
-// and MLP::forward equals the chain gate/up -> mlxr_swiglu -> down.  Built and run by
+// and MLP::forward equals the chain (fused mlxr_qgemm_swiglu at M <= 4, else gate/up ->
+// mlxr_swiglu) -> down.  Built and run by
 // tests/test_layers.py (GPU); prints "OK <n>" on success.
 #include <hip/hip_runtime.h>
 
@@ -103,9 +104,16 @@ int main(int argc, char** argv) {
   for (int M : {2, 24}) {
     array x = act(M, H, 50 + M);
     array y = mlp.forward(x);
-    array g = mlp.gate_proj().forward(x), u = mlp.up_proj().forward(x);
     array h({M, I}, Dtype::bfloat16);
-    EXPECT(mlxr_swiglu(g.data<void>(), u.data<void>(), h.data<void>(), (size_t)M * I, MLXR_BF16, nullptr) == 0);
+    if (M <= 4) {
+      EXPECT(mlxr_qgemm_swiglu(MLXR_Q4_K, I, H, mlp.gate_proj().weight().data<void>(),
+                               mlp.up_proj().weight().data<void>(), x.data<void>(), MLXR_BF16, h.data<void>(),
+                               MLXR_BF16, M, nullptr, 0, nullptr) == 0);
+    } else {
+      array g = mlp.gate_proj().forward(x), u = mlp.up_proj().forward(x);
+      EXPECT(mlxr_swiglu(g.data<void>(), u.data<void>(), h.data<void>(), (size_t)M * I, MLXR_BF16, nullptr) == 0);
+      hipDeviceSynchronize();
+    }
     array y2 = mlp.down_proj().forward(h);
     hipDeviceSynchronize();
     EXPECT(to_host(y) == to_host(y2));

@@ -104,9 +104,13 @@ def test_mlp_forward_stagewise(cuda, M):
     hf = h.float().cpu().numpy()
     ref = orc.gemm_f64(int(Q4K), M, H, I, ws["d"], hf, w_to_bf16=wb)
     assert orc.normwise_rel_err(y.float().cpu().numpy(), ref) <= TOL
-    # the layer is exactly that chain (grouped gate/up at M <= 4 equals the separate calls)
-    y2 = mlp.down_proj(h)
-    assert torch.equal(y, y2)
+    if M > 4:
+        # the layer is exactly that chain
+        assert torch.equal(y, mlp.down_proj(h))
+    else:
+        # one fused launch: the gating sees fp32 gate/up (no bf16 round trip in between)
+        hf = mx.q_gemm_swiglu(x, mlp.gate_proj.weight, mlp.up_proj.weight)
+        assert torch.equal(y, mlp.down_proj(hf))
 
 
 @pytest.mark.gpu
@@ -125,3 +129,28 @@ def test_cpp_layers(cuda, tmp_path):
     subprocess.run(cmd, check=True, capture_output=True)
     r = subprocess.run([str(exe), str(p)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.startswith("OK"), r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qt", [mx.QuantType.Q4_K, mx.QuantType.Q6_K, mx.QuantType.Q8_0, mx.QuantType.Q4_0,
+                                mx.QuantType.Q4_1])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 130])
+def test_q_gemm_swiglu_matches_oracle(cuda, qt, M):
+    """h = swish(x Wg^T) * (x Wu^T) against fp64 on the oracle's gate and up; one launch for
+    M <= 4, projections + gating (workspace) above."""
+    import torch
+    N, K = 768, 1024
+    wg, wu = mx.synth_gguf(qt, N, K, 61), mx.synth_gguf(qt, N, K, 62)
+    pg = mx.pack_weights(wg, N, K, qt, device=cuda)
+    pu = mx.pack_weights(wu, N, K, qt, device=cuda)
+    x, xf = _act(torch, (M, K), 63 + M, cuda)
+    for odt in (torch.bfloat16, torch.float32):
+        h = mx.q_gemm_swiglu(x, pg, pu, out_dtype=odt)
+        wb = M > 4
+        g = orc.gemm_f64(int(qt), M, N, K, wg, xf, w_to_bf16=wb).astype(np.float64)
+        u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=wb).astype(np.float64)
+        if M > 4:  # the unfused path rounds gate and up to the output type first
+            rnd = (lambda a: torch.tensor(a).to(odt).double().numpy())
+            g, u = rnd(g), rnd(u)
+        ref = _swiglu64(g, u)
+        assert orc.normwise_rel_err(h.float().cpu().numpy(), ref) <= TOL
