@@ -22,7 +22,7 @@
  *   - Thread-safe: the library has no mutable global state besides the thread-local
  *     error string.
  *   - Dequantized weights follow the GGUF block_q4_0 / block_q4_1 / block_q8_0 /
- *     block_q4_K / block_q6_K definitions exactly (fp32 results are bit-exact to those
+ *     block_q4_K / block_q5_K / block_q6_K definitions exactly (fp32 results are bit-exact to those
  *     formulas).
  */
 #ifndef MLXR_QGEMM_H
@@ -36,7 +36,7 @@ extern "C" {
 #endif
 
 /* Quantization types: same numeric values as mlxr::kernels::QuantType
- * (reference q_gemm_dequant_primitive.h:18-35).  Implemented: Q4_0, Q4_1, Q8_0, Q4_K, Q6_K.
+ * (reference q_gemm_dequant_primitive.h:18-35).  Implemented: Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K.
  * Q4_0/Q4_1 follow GGUF block_q4_0/block_q4_1 (byte j holds elements j and j+16); the
  * reference's CPU routines (.mm:189-216) read them interleaved (elements 2j, 2j+1). */
 enum {
@@ -78,8 +78,8 @@ const char* mlxr_qgemm_last_error(void);
  * calculate_tensor_size (daemon/registry/gguf_parser.cpp:179-241, Q6_K = 210 B). */
 int mlxr_qgemm_gguf_size(int qtype, int N, int K, size_t* bytes);
 
-/* Elements per quantization group: Q8_0 -> 32, Q4_K/Q6_K -> 256
- * (reference get_default_group_size, .mm:80-92). */
+/* Elements per quantization group: Q4_0/Q4_1/Q8_0 -> 32, Q4_K/Q5_K/Q6_K -> 256
+ * (reference get_default_group_size, .mm:80-92; it has no Q5_K). */
 int mlxr_qgemm_group_size(int qtype);
 
 /* Name of a quant type ("Q4_K", ...; "Unknown" otherwise) (reference .mm:94-114). */
@@ -184,6 +184,7 @@ int mlxr_swiglu(const void* gate_dev, const void* up_dev, void* out_dev, size_t 
  *   Q6_K: ql, qh bytes uniform, scales uniform in [-32, 31], d = RNE_fp16(|N(0,1)|*1e-3)
  *   Q4_0: d = RNE_fp16(|N(0,1)| * 2e-3), 16 qs bytes uniform
  *   Q4_1: d = RNE_fp16(|N(0,1)| * 2e-3), m = RNE_fp16(N(0,1) * 8e-3), 16 qs bytes uniform
+ *   Q5_K: as Q4_K, plus 32 uniform qh bytes
  * out_host must hold mlxr_qgemm_gguf_size bytes. */
 int mlxr_synth_gguf(int qtype, int N, int K, uint64_t seed, void* out_host);
 

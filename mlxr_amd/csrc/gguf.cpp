@@ -459,6 +459,7 @@ int mlxr_gguf_quant_type(uint32_t ggml_type) {
     case MLXR_GGML_Q4_1: return MLXR_Q4_1;
     case MLXR_GGML_Q8_0: return MLXR_Q8_0;
     case MLXR_GGML_Q4_K: return MLXR_Q4_K;
+    case MLXR_GGML_Q5_K: return MLXR_Q5_K;
     case MLXR_GGML_Q6_K: return MLXR_Q6_K;
     default:
       return set_error(MLXR_E_UNSUPPORTED, "ggml type %s has no quantized matmul", mlxr_gguf_type_name(ggml_type));

@@ -65,6 +65,7 @@ float QGemmDequantPrimitive::get_bytes_per_weight(QuantType type) {
     case QuantType::Q4_1: return 20 / 32.0f;
     case QuantType::Q8_0: return 34 / 32.0f;
     case QuantType::Q4_K: return 144 / 256.0f;
+    case QuantType::Q5_K: return 176 / 256.0f;
     case QuantType::Q6_K: return 210 / 256.0f;
     default: throw std::runtime_error("Unsupported quantization type");
   }
@@ -79,7 +80,7 @@ const char* quant_type_name(QuantType type) { return mlxr_qgemm_type_name((int)t
 size_t compute_quantized_weight_size(int N, int K, QuantType quant_type) {
   switch (quant_type) {
     case QuantType::Q4_0: case QuantType::Q4_1: case QuantType::Q8_0:
-    case QuantType::Q4_K: case QuantType::Q6_K: break;
+    case QuantType::Q4_K: case QuantType::Q5_K: case QuantType::Q6_K: break;
     default: throw std::runtime_error("Unsupported quantization type");
   }
   size_t bytes = 0;

@@ -53,7 +53,8 @@ int hip_fail(hipError_t e, const char* where) {
 }
 
 bool implemented(int qtype) {
-  return qtype == MLXR_Q4_0 || qtype == MLXR_Q4_1 || qtype == MLXR_Q8_0 || qtype == MLXR_Q4_K || qtype == MLXR_Q6_K;
+  return qtype == MLXR_Q4_0 || qtype == MLXR_Q4_1 || qtype == MLXR_Q8_0 || qtype == MLXR_Q4_K || qtype == MLXR_Q5_K ||
+         qtype == MLXR_Q6_K;
 }
 
 int check_type_shape(int qtype, int N, int K, mlxr::PackedLayout* L) {
@@ -88,9 +89,9 @@ const char* mlxr_qgemm_type_name(int qtype) {
 }
 
 int mlxr_qgemm_group_size(int qtype) {
-  // reference get_default_group_size (.mm:80-92): 256 for the K-quants, 32 otherwise
-  // (types beyond Q6_K fall back to 32 there as well).
-  return (qtype == MLXR_Q4_K || qtype == MLXR_Q6_K) ? 256 : 32;
+  // reference get_default_group_size (.mm:80-92): 256 for Q4_K/Q6_K, 32 otherwise.  Q5_K,
+  // which the reference never runs (its default would be 32), takes its GGUF super-block.
+  return (qtype == MLXR_Q4_K || qtype == MLXR_Q5_K || qtype == MLXR_Q6_K) ? 256 : 32;
 }
 
 int mlxr_qgemm_gguf_size(int qtype, int N, int K, size_t* bytes) {

@@ -52,6 +52,11 @@ __host__ __device__ constexpr int q6h_shift(int e) {
   return 2 * ((e & 7) >> 1) + 16 * (e & 1) + 8 * ((e >> 3) & 1);
 }
 
+// Bit of the fifth bit of weight e (0..31 in a Q5_K sub-block) in its qh word.
+__host__ __device__ constexpr int q5h_bit(int e) {
+  return 2 * (e >> 3) + ((e >> 1) & 1) + 8 * (((e >> 2) & 1) + 2 * (e & 1));
+}
+
 // Q4_K lane-sliced header (8 x u16 per super-block): d | dmin << 16 from the high
 // nibbles of all eight entries.
 __device__ __forceinline__ uint32_t q4k_dd(const uint4& h) {
@@ -84,6 +89,12 @@ struct RawSub<QT_Q8_0> {
 };
 
 template <>
+struct RawSub<QT_Q5_K> {
+  uint4 q;      // low nibbles, as Q4_K
+  uint32_t qh;  // fifth bits (q5h_bit order)
+  uint4 h;      // the super-block's lane-sliced header, as Q4_K
+};
+template <>
 struct RawSub<QT_Q4_0> {
   uint4 q;     // 4 pair-interleaved words
   uint32_t d;  // fp16 bits
@@ -101,6 +112,11 @@ __device__ __forceinline__ void load_raw_sub(const uint8_t* const* planes, int K
     const size_t nsb = (size_t)(K / 256);
     r.q = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
     r.h = *(const uint4*)(planes[1] + ((size_t)n * nsb + (sb >> 3)) * 16);
+  } else if constexpr (QT == QT_Q5_K) {
+    const size_t nsb = (size_t)(K / 256);
+    r.q = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
+    r.qh = *(const uint32_t*)(planes[1] + ((size_t)n * nsub + sb) * 4);
+    r.h = *(const uint4*)(planes[2] + ((size_t)n * nsb + (sb >> 3)) * 16);
   } else if constexpr (QT == QT_Q6_K) {
     const size_t nsb = (size_t)(K / 256);
     r.ql = *(const uint4*)(planes[0] + ((size_t)n * nsub + sb) * 16);
@@ -124,7 +140,7 @@ __device__ __forceinline__ void load_raw_sub(const uint8_t* const* planes, int K
 // super-block (sb % 8).
 template <int QT>
 __device__ __forceinline__ void dequant_raw(const RawSub<QT>& r, int j, float* w) {
-  if constexpr (QT == QT_Q4_K) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
     const uint32_t dd = q4k_dd(r.h);
     const uint32_t hw[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
     const uint32_t f = (hw[j >> 1] >> (16 * (j & 1))) & 0xfffu;
@@ -133,7 +149,8 @@ __device__ __forceinline__ void dequant_raw(const RawSub<QT>& r, int j, float* w
     const uint32_t qw[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
-      const uint32_t v = (qw[e >> 3] >> pi_shift(e & 7)) & 15u;
+      uint32_t v = (qw[e >> 3] >> pi_shift(e & 7)) & 15u;
+      if constexpr (QT == QT_Q5_K) v |= ((r.qh >> q5h_bit(e)) & 1u) << 4;
       w[e] = __builtin_fmaf(dsc, (float)v, -dm);
     }
   } else if constexpr (QT == QT_Q6_K) {

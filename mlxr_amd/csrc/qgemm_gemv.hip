@@ -128,6 +128,12 @@ struct WLoad<QT_Q8_0> {
   uint32_t d;
 };
 template <>
+struct WLoad<QT_Q5_K> {
+  uint4 q;
+  uint32_t qh;  // fifth bits
+  uint32_t h;   // this lane's u16 of the lane-sliced header
+};
+template <>
 struct WLoad<QT_Q4_0> {
   uint4 q;
   uint32_t d;  // fp16 bits
@@ -162,6 +168,11 @@ __device__ __forceinline__ void load_w(const PlanePtrs& P, int K, int n, int sb,
     w.qh = *(const uint2*)(P.p[1] + ((size_t)n * nsub + sb) * 8);
     w.sc = *(const uint16_t*)(P.p[2] + ((size_t)n * nsb + (sb >> 3)) * 16 + 2 * (sb & 7));
     w.d = *(const uint16_t*)(P.p[3] + ((size_t)n * nsb + (sb >> 3)) * 2);
+  } else if constexpr (QT == QT_Q5_K) {
+    const size_t nsb = (size_t)(K >> 8);
+    w.q = ldw16<NT>(P.p[0] + ((size_t)n * nsub + sb) * 16);
+    w.qh = *(const uint32_t*)(P.p[1] + ((size_t)n * nsub + sb) * 4);
+    w.h = *(const uint16_t*)(P.p[2] + ((size_t)n * nsb + (sb >> 3)) * 16 + 2 * (sb & 7));
   } else if constexpr (QT == QT_Q4_0) {
     w.q = ldw16<NT>(P.p[0] + ((size_t)n * nsub + sb) * 16);
     w.d = *(const uint16_t*)(P.p[1] + ((size_t)n * nsub + sb) * 2);
@@ -185,6 +196,10 @@ __device__ __forceinline__ void zero_w(WLoad<QT>& w) {
     w.qh = make_uint2(0, 0);
     w.sc = 0;
     w.d = 0;
+  } else if constexpr (QT == QT_Q5_K) {
+    w.q = make_uint4(0, 0, 0, 0);
+    w.qh = 0;
+    w.h = 0;
   } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
     w.q = make_uint4(0, 0, 0, 0);
     w.d = 0;
@@ -202,15 +217,24 @@ struct WDec {
                  // Q4_0: d, 8d.  Q4_1: d, -m  (so Q4_0/Q4_1/Q4_K share one contribution)
 };
 
+// Fifth bits of pair s of word t of a Q5_K sub-block, at bits 4 and 20 (q5h_bit order).
+__device__ __forceinline__ uint32_t q5_pair_bits(uint32_t qh, int t, int s) {
+  const int r = 2 * t + (s & 1) + 8 * (s >> 1) - 4;
+  return (r >= 0 ? (qh >> r) : (qh << (-r))) & 0x00100010u;
+}
+
 template <int QT, int XT>
 __device__ __forceinline__ void decode_w(const WLoad<QT>& w, int j, WDec& o) {
-  if constexpr (QT == QT_Q4_K) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
     constexpr uint32_t MAGIC = (XT == X_BF16) ? 0x43004300u : 0x64006400u;
     const uint32_t qw[4] = {w.q.x, w.q.y, w.q.z, w.q.w};
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) o.p[4 * t + s] = ((qw[t] >> (4 * s)) & 0x000F000Fu) | MAGIC;
+      for (int s = 0; s < 4; ++s) {
+        o.p[4 * t + s] = ((qw[t] >> (4 * s)) & 0x000F000Fu) | MAGIC;
+        if constexpr (QT == QT_Q5_K) o.p[4 * t + s] |= q5_pair_bits(w.qh, t, s);
+      }
     // d | dmin << 16: nibble j of it sits in bits 12..15 of lane j's entry; OR the eight
     // lanes of the super-block together (xor 1, xor 2 within quads, then mirror within 8).
     uint32_t dd = (w.h >> 12) << (4 * j);
@@ -266,7 +290,7 @@ __device__ __forceinline__ void decode_w(const WLoad<QT>& w, int j, WDec& o) {
 // Contribution of one decoded row/sub-block against one activation sub-block.
 template <int QT, int XT>
 __device__ __forceinline__ float contrib(const uint32_t* xv, const WDec& w, float X0, float X1) {
-  if constexpr (QT == QT_Q4_K || QT == QT_Q4_0 || QT == QT_Q4_1) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q4_0 || QT == QT_Q4_1) {
     constexpr float OFF = (XT == X_BF16) ? 128.f : 1024.f;
     const float S = dot_range<XT, 0, 16>(xv, w.p);
     return w.s0 * (S - OFF * (X0 + X1)) - w.s1 * (X0 + X1);
@@ -409,6 +433,12 @@ struct CLoad<QT_Q8_0> {
   uint16_t d;
 };
 template <>
+struct CLoad<QT_Q5_K> {
+  uint4 q;
+  uint32_t qh;
+  uint16_t h;
+};
+template <>
 struct CLoad<QT_Q4_0> {
   uint4 q;
   uint16_t d;
@@ -461,6 +491,11 @@ __device__ __forceinline__ void load_chunk(const rsrc_t* R, int row, int seg, in
     b.qh = make_uint2(h[0], h[1]);
     b.sc = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, 0);
     b.d = __builtin_amdgcn_raw_buffer_load_b16(R[3], ok ? (lane >> 3) * 2 : OOB, gbase * 2u, 0);
+  } else if constexpr (QT == QT_Q5_K) {
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    b.q = make_uint4(q[0], q[1], q[2], q[3]);
+    b.qh = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? lane * 4 : OOB, sbase * 4u, 0);
+    b.h = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, 0);
   } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
     const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
     b.q = make_uint4(q[0], q[1], q[2], q[3]);
@@ -477,12 +512,15 @@ __device__ __forceinline__ void load_chunk(const rsrc_t* R, int row, int seg, in
 
 template <int QT, int XT>
 __device__ __forceinline__ void decode_chunk(const CLoad<QT>& b, int j, uint32_t MASK, uint32_t MAGIC, WDec& o) {
-  if constexpr (QT == QT_Q4_K) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
     const uint32_t qw[4] = {b.q.x, b.q.y, b.q.z, b.q.w};
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) o.p[4 * t + s] = and_or(qw[t] >> (4 * s), MASK, MAGIC);
+      for (int s = 0; s < 4; ++s) {
+        if constexpr (QT == QT_Q5_K) o.p[4 * t + s] = and_or(qw[t] >> (4 * s), MASK, MAGIC | q5_pair_bits(b.qh, t, s));
+        else o.p[4 * t + s] = and_or(qw[t] >> (4 * s), MASK, MAGIC);
+      }
     // d | dmin << 16: nibble j of it sits in bits 12..15 of lane j's entry; OR the eight
     // lanes of the super-block together (xor 1, xor 2 within quads, then mirror within 8).
     const uint32_t hv = b.h;
@@ -887,6 +925,7 @@ hipError_t launch_gemv(const RunArgs& a, hipStream_t s) {
   switch (a.L.qtype) {
     case QT_Q4_K: return f16 ? launch_x<QT_Q4_K, X_F16>(p, a, R, s) : launch_x<QT_Q4_K, X_BF16>(p, a, R, s);
     case QT_Q6_K: return f16 ? launch_x<QT_Q6_K, X_F16>(p, a, R, s) : launch_x<QT_Q6_K, X_BF16>(p, a, R, s);
+    case QT_Q5_K: return f16 ? launch_x<QT_Q5_K, X_F16>(p, a, R, s) : launch_x<QT_Q5_K, X_BF16>(p, a, R, s);
     case QT_Q4_0: return f16 ? launch_x<QT_Q4_0, X_F16>(p, a, R, s) : launch_x<QT_Q4_0, X_BF16>(p, a, R, s);
     case QT_Q4_1: return f16 ? launch_x<QT_Q4_1, X_F16>(p, a, R, s) : launch_x<QT_Q4_1, X_BF16>(p, a, R, s);
     default: return f16 ? launch_x<QT_Q8_0, X_F16>(p, a, R, s) : launch_x<QT_Q8_0, X_BF16>(p, a, R, s);
@@ -922,6 +961,7 @@ hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s
   switch (a.L.qtype) {
     case QT_Q4_K: return f16 ? launch_lds<QT_Q4_K, X_F16>(items, n, s) : launch_lds<QT_Q4_K, X_BF16>(items, n, s);
     case QT_Q6_K: return f16 ? launch_lds<QT_Q6_K, X_F16>(items, n, s) : launch_lds<QT_Q6_K, X_BF16>(items, n, s);
+    case QT_Q5_K: return f16 ? launch_lds<QT_Q5_K, X_F16>(items, n, s) : launch_lds<QT_Q5_K, X_BF16>(items, n, s);
     case QT_Q4_0: return f16 ? launch_lds<QT_Q4_0, X_F16>(items, n, s) : launch_lds<QT_Q4_0, X_BF16>(items, n, s);
     case QT_Q4_1: return f16 ? launch_lds<QT_Q4_1, X_F16>(items, n, s) : launch_lds<QT_Q4_1, X_BF16>(items, n, s);
     default: return f16 ? launch_lds<QT_Q8_0, X_F16>(items, n, s) : launch_lds<QT_Q8_0, X_BF16>(items, n, s);
@@ -933,6 +973,7 @@ hipError_t launch_gemv_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_
   switch (gate.L.qtype) {
     case QT_Q4_K: return f16 ? launch_lds_swiglu<QT_Q4_K, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q4_K, X_BF16>(gate, up, s);
     case QT_Q6_K: return f16 ? launch_lds_swiglu<QT_Q6_K, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q6_K, X_BF16>(gate, up, s);
+    case QT_Q5_K: return f16 ? launch_lds_swiglu<QT_Q5_K, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q5_K, X_BF16>(gate, up, s);
     case QT_Q4_0: return f16 ? launch_lds_swiglu<QT_Q4_0, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q4_0, X_BF16>(gate, up, s);
     case QT_Q4_1: return f16 ? launch_lds_swiglu<QT_Q4_1, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q4_1, X_BF16>(gate, up, s);
     default: return f16 ? launch_lds_swiglu<QT_Q8_0, X_F16>(gate, up, s) : launch_lds_swiglu<QT_Q8_0, X_BF16>(gate, up, s);

@@ -18,6 +18,11 @@
 //                                        = sc_j | m_j << 6 | nibble j of (d | dmin << 16) << 12,
 //                                        so the lane that owns sub-block j loads 2 bytes and
 //                                        rebuilds d, dmin with an OR across the 8 lanes
+//   Q5_K  plane 0  qs   [N][nsub][16 B]  low 4 bits, as Q4_K
+//         plane 1  qh   [N][nsub][4 B]   fifth bits: weight e = 8t + f of the sub-block at
+//                                        bit 2t + ((f>>1)&1) + 8(((f>>2)&1) + 2(f&1)), so one
+//                                        shift lines them up with a word's nibble bytes
+//         plane 2  hdr  [N][K/256][16 B] lane-sliced header, as Q4_K
 //   Q6_K  plane 0  ql   [N][nsub][16 B]  low 4 bits, 4 pair-interleaved words
 //         plane 1  qh   [N][nsub][8 B]   high 2 bits; for word t (weights 8t..8t+7) of
 //                                        the sub-block: u32 index t/2, weight 8t+2s at
@@ -45,7 +50,7 @@ namespace mlxr {
 
 // Same numeric values as mlxr::kernels::QuantType (core/kernels/primitives/
 // q_gemm_dequant_primitive.h:18-35 in the reference).
-enum QType : int { QT_Q4_0 = 0, QT_Q4_1 = 1, QT_Q8_0 = 2, QT_Q4_K = 3, QT_Q6_K = 4 };
+enum QType : int { QT_Q4_0 = 0, QT_Q4_1 = 1, QT_Q8_0 = 2, QT_Q4_K = 3, QT_Q6_K = 4, QT_Q5_K = 10 };
 
 struct PackedLayout {
   int qtype, N, K;
@@ -59,7 +64,7 @@ MLXR_HD inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // K-quants carry a per-super-block header (scales of eight sub-blocks); the 32-weight
 // block types carry their scale with every block.
-MLXR_HD constexpr bool is_kquant(int qtype) { return qtype == QT_Q4_K || qtype == QT_Q6_K; }
+MLXR_HD constexpr bool is_kquant(int qtype) { return qtype == QT_Q4_K || qtype == QT_Q5_K || qtype == QT_Q6_K; }
 
 // Fills L; returns false if the type is not one the kernels implement or K does not
 // split into whole blocks.
@@ -72,6 +77,10 @@ MLXR_HD inline bool make_layout(int qtype, int N, int K, PackedLayout* L) {
     if (K % 256) return false;
     const size_t nsb = (size_t)(K / 256);
     L->nplanes = 2; L->size[0] = n * nsb * 128; L->size[1] = n * nsb * 16;
+  } else if (qtype == QT_Q5_K) {
+    if (K % 256) return false;
+    const size_t nsb = (size_t)(K / 256);
+    L->nplanes = 3; L->size[0] = n * nsb * 128; L->size[1] = n * nsb * 32; L->size[2] = n * nsb * 16;
   } else if (qtype == QT_Q6_K) {
     if (K % 256) return false;
     const size_t nsb = (size_t)(K / 256);
@@ -99,7 +108,7 @@ MLXR_HD inline bool make_layout(int qtype, int N, int K, PackedLayout* L) {
 MLXR_HD inline int gguf_block_elems(int qtype) {
   switch (qtype) {
     case QT_Q4_0: case QT_Q4_1: case QT_Q8_0: return 32;
-    case QT_Q4_K: case QT_Q6_K: return 256;
+    case QT_Q4_K: case QT_Q5_K: case QT_Q6_K: return 256;
     default: return 0;
   }
 }
@@ -110,6 +119,7 @@ MLXR_HD inline int gguf_block_bytes(int qtype) {
     case QT_Q8_0: return 34;
     case QT_Q4_K: return 144;
     case QT_Q6_K: return 210;
+    case QT_Q5_K: return 176;
     default: return 0;
   }
 }

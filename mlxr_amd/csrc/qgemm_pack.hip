@@ -55,6 +55,48 @@ __global__ void pack_q4k_kernel(const uint8_t* __restrict__ src, uint8_t* __rest
   }
 }
 
+// One thread per (row, super-block).  Source: 176-byte block_q5_K records
+// {d, dmin, scales[12], qh[32], qs[128]}: header and qs as Q4_K; the fifth bit of element
+// l of sub-block j is bit j of qh[l].
+__global__ void pack_q5k_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs_out,
+                                uint8_t* __restrict__ qh_out, uint8_t* __restrict__ hdr_out, int N, int nsb) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)N * nsb) return;
+  const uint8_t* b = src + idx * 176;
+  const uint8_t* s = b + 4;
+  const uint8_t* qh = b + 16;
+  const uint8_t* q = b + 48;
+  const uint32_t dd = rd_u16(b, 0) | (rd_u16(b, 2) << 16);
+  uint16_t* h = (uint16_t*)(hdr_out + idx * 16);
+  for (int j = 0; j < 8; ++j) {
+    uint32_t sc, m;
+    if (j < 4) {
+      sc = s[j] & 63u;
+      m = s[j + 4] & 63u;
+    } else {
+      sc = (s[j + 4] & 15u) | ((uint32_t)(s[j - 4] >> 6) << 4);
+      m = (uint32_t)(s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+    }
+    h[j] = (uint16_t)(sc | (m << 6) | (((dd >> (4 * j)) & 15u) << 12));
+  }
+  uint32_t* o = (uint32_t*)(qs_out + idx * 128);
+  uint32_t* oh = (uint32_t*)(qh_out + idx * 32);
+  for (int j = 0; j < 8; ++j) {
+    const int c = j >> 1, hi = j & 1;
+    uint32_t hw = 0;
+    for (int t = 0; t < 4; ++t) {
+      uint32_t w = 0;
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t byte = rd_u8(q, 32 * c + 8 * t + e);
+        w |= (hi ? (byte >> 4) : (byte & 15u)) << pi_shift(e);
+        hw |= ((rd_u8(qh, 8 * t + e) >> j) & 1u) << q5h_bit(8 * t + e);
+      }
+      o[4 * j + t] = w;
+    }
+    oh[j] = hw;
+  }
+}
+
 // One thread per (row, super-block).  Source: 210-byte block_q6_K records.
 __global__ void pack_q6k_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ ql_out,
                                 uint8_t* __restrict__ qh_out, uint8_t* __restrict__ sc_out,
@@ -157,6 +199,11 @@ hipError_t launch_pack(const PackedLayout& L, const uint8_t* gguf_dev, uint8_t* 
     const size_t total = (size_t)L.N * nsb;
     pack_q4k_kernel<<<dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s>>>(
         gguf_dev, packed_dev + L.off[0], packed_dev + L.off[1], L.N, nsb);
+  } else if (L.qtype == QT_Q5_K) {
+    const int nsb = L.K / 256;
+    const size_t total = (size_t)L.N * nsb;
+    pack_q5k_kernel<<<dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0, s>>>(
+        gguf_dev, packed_dev + L.off[0], packed_dev + L.off[1], packed_dev + L.off[2], L.N, nsb);
   } else if (L.qtype == QT_Q6_K) {
     const int nsb = L.K / 256;
     const size_t total = (size_t)L.N * nsb;
@@ -192,6 +239,8 @@ hipError_t launch_dequant(const PackedLayout& L, const uint8_t* packed_dev, void
     dequant_kernel<QT_Q4_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   else if (L.qtype == QT_Q6_K)
     dequant_kernel<QT_Q6_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
+  else if (L.qtype == QT_Q5_K)
+    dequant_kernel<QT_Q5_K><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   else if (L.qtype == QT_Q4_0)
     dequant_kernel<QT_Q4_0><<<grid, dim3(threads), 0, s>>>(P, L.N, L.K, out, out_dtype, 0x0F0F0F0Fu);
   else if (L.qtype == QT_Q4_1)

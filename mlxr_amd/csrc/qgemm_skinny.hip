@@ -262,6 +262,7 @@ hipError_t launch_skinny(const RunArgs& a, hipStream_t s) {
   switch (a.L.qtype) {
     case QT_Q4_K: return f16 ? launch_s<QT_Q4_K, X_F16>(sp, s) : launch_s<QT_Q4_K, X_BF16>(sp, s);
     case QT_Q6_K: return f16 ? launch_s<QT_Q6_K, X_F16>(sp, s) : launch_s<QT_Q6_K, X_BF16>(sp, s);
+    case QT_Q5_K: return f16 ? launch_s<QT_Q5_K, X_F16>(sp, s) : launch_s<QT_Q5_K, X_BF16>(sp, s);
     case QT_Q4_0: return f16 ? launch_s<QT_Q4_0, X_F16>(sp, s) : launch_s<QT_Q4_0, X_BF16>(sp, s);
     case QT_Q4_1: return f16 ? launch_s<QT_Q4_1, X_F16>(sp, s) : launch_s<QT_Q4_1, X_BF16>(sp, s);
     default: return f16 ? launch_s<QT_Q8_0, X_F16>(sp, s) : launch_s<QT_Q8_0, X_BF16>(sp, s);

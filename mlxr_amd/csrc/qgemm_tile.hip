@@ -495,6 +495,7 @@ hipError_t launch_chunk(const TileParams& tp, int bm, int S, int qtype, bool f16
   switch (qtype) {
     case QT_Q4_K: return f16 ? launch_q<QT_Q4_K, X_F16>(tp, bm, S, s) : launch_q<QT_Q4_K, X_BF16>(tp, bm, S, s);
     case QT_Q6_K: return f16 ? launch_q<QT_Q6_K, X_F16>(tp, bm, S, s) : launch_q<QT_Q6_K, X_BF16>(tp, bm, S, s);
+    case QT_Q5_K: return f16 ? launch_q<QT_Q5_K, X_F16>(tp, bm, S, s) : launch_q<QT_Q5_K, X_BF16>(tp, bm, S, s);
     case QT_Q4_0: return f16 ? launch_q<QT_Q4_0, X_F16>(tp, bm, S, s) : launch_q<QT_Q4_0, X_BF16>(tp, bm, S, s);
     case QT_Q4_1: return f16 ? launch_q<QT_Q4_1, X_F16>(tp, bm, S, s) : launch_q<QT_Q4_1, X_BF16>(tp, bm, S, s);
     default: return f16 ? launch_q<QT_Q8_0, X_F16>(tp, bm, S, s) : launch_q<QT_Q8_0, X_BF16>(tp, bm, S, s);

@@ -36,9 +36,9 @@ __device__ __forceinline__ u32x4_t bload16(rsrc_t r, uint32_t voff, uint32_t sof
 
 // VMEM instructions of load_raw / load_hdr (one weight row).
 template <int QT>
-constexpr int raw_loads() { return QT == QT_Q4_K ? 1 : QT == QT_Q6_K ? 2 : QT == QT_Q8_0 ? 3 : 2; }
+constexpr int raw_loads() { return QT == QT_Q4_K ? 1 : QT == QT_Q6_K ? 2 : QT == QT_Q8_0 ? 3 : 2; }  // Q5_K, Q4_0/1: 2
 template <int QT>
-constexpr int hdr_loads() { return QT == QT_Q4_K ? 1 : QT == QT_Q6_K ? 2 : 0; }  // K-quants only
+constexpr int hdr_loads() { return (QT == QT_Q4_K || QT == QT_Q5_K) ? 1 : QT == QT_Q6_K ? 2 : 0; }  // K-quants only
 
 template <int QT>
 __device__ __forceinline__ void load_raw(const rsrc_t* R, uint32_t row_sub, int sb, bool ok, Raw<QT>& r) {
@@ -49,6 +49,9 @@ __device__ __forceinline__ void load_raw(const rsrc_t* R, uint32_t row_sub, int 
   } else if constexpr (QT == QT_Q6_K) {
     r.ql = bload16(R[0], ok ? s * 16u : OOB);
     r.qh = __builtin_amdgcn_raw_buffer_load_b64(R[1], ok ? s * 8u : OOB, 0, 0);
+  } else if constexpr (QT == QT_Q5_K) {
+    r.q = bload16(R[0], ok ? s * 16u : OOB);
+    r.qh = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? s * 4u : OOB, 0, 0);
   } else if constexpr (QT == QT_Q4_0) {
     r.q = bload16(R[0], ok ? s * 16u : OOB);
     r.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? s * 2u : OOB, 0, 0);
@@ -69,6 +72,8 @@ __device__ __forceinline__ void load_hdr(const rsrc_t* R, uint32_t row_sb, int g
   const uint32_t s = row_sb + (uint32_t)g;
   if constexpr (QT == QT_Q4_K) {
     h.h = bload16(R[1], ok ? s * 16u : OOB);
+  } else if constexpr (QT == QT_Q5_K) {
+    h.h = bload16(R[2], ok ? s * 16u : OOB);
   } else if constexpr (QT == QT_Q6_K) {
     h.h = bload16(R[2], ok ? s * 16u : OOB);
     h.d = __builtin_amdgcn_raw_buffer_load_b16(R[3], ok ? s * 2u : OOB, 0, 0);

@@ -6,6 +6,7 @@
 // 8kk+7) as four packed pairs of the MFMA element type (bf16, or fp16 for fp16
 // activations).  Each value is the exact GGUF fp32 weight, rounded to nearest even:
 //   Q4_K  fma(d*sc, q, -(dmin*m))       (d*sc, q*d*sc and dmin*m exact; one rounding)
+//   Q5_K  as Q4_K with q in 0..31
 //   Q6_K  (d*sc) * (q - 32)             (exact; q - 32 formed exactly in fp32)
 //   Q8_0  d * q                         (exact)
 //   Q4_0  (q - 8) * d                   (exact)
@@ -71,6 +72,17 @@ struct Raw<QT_Q8_0> {
   }
 };
 
+// Q5_K: the Q4_K nibbles plus the sub-block's fifth bits (q5h_bit order).
+template <>
+struct Raw<QT_Q5_K> {
+  u32x4_t q;
+  uint32_t qh;
+  __device__ void pin_all() {
+    pin(q);
+    pin(qh);
+  }
+};
+
 // Q4_0 / Q4_1: one 32-weight block (4 pair-interleaved words) and its scale word
 // (fp16 d, plus fp16 m in the high half for Q4_1).
 template <>
@@ -111,7 +123,7 @@ struct Scales {
 
 template <int QT>
 __device__ __forceinline__ void decode_hdr(const Hdr<QT>& h, int half, Scales<QT>& s) {
-  if constexpr (QT == QT_Q4_K) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
     const uint32_t dd = q4k_dd(make_uint4(h.h[0], h.h[1], h.h[2], h.h[3]));
     const float d = f16_bits_to_f32(dd & 0xffffu), dmin = f16_bits_to_f32(dd >> 16);
     const uint32_t w[4] = {h.h[0], h.h[1], h.h[2], h.h[3]};
@@ -155,6 +167,18 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
     t.u1 = (w >> 4) & nib;
     t.a = s.a[q];
     t.c = s.b[q];
+  } else if constexpr (QT == QT_Q5_K) {
+    // the fifth bits of word kk's nibble bytes sit at bits 2kk (+1 for u1) + 8b of qh
+    uint32_t w = r.q[kk], hb = r.qh;
+    pin(w);
+    pin(hb);
+    constexpr int sh = 2 * kk - 4;  // moves bit 2kk + 8b to bit 4 + 8b
+    const uint32_t h0 = sh >= 0 ? (hb >> sh) : (hb << (-sh));
+    const uint32_t h1 = sh + 1 >= 0 ? (hb >> (sh + 1)) : (hb << (-(sh + 1)));
+    t.u0 = (w & nib) | (h0 & 0x10101010u);
+    t.u1 = ((w >> 4) & nib) | (h1 & 0x10101010u);
+    t.a = s.a[q];
+    t.c = s.b[q];
   } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
     uint32_t w = r.q[kk];
     pin(w);
@@ -184,7 +208,7 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
 
 template <int QT, int XT, int kk, int qq>
 __device__ __forceinline__ uint32_t word_quarter(const WordTmp<QT>& t, uint32_t nib) {
-  if constexpr (QT == QT_Q4_K || QT == QT_Q4_1) {
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q4_1) {
     // u0 bytes: weights 0, 4, 1, 5; u1 bytes: 2, 6, 3, 7
     const uint32_t v = (qq & 1) ? t.u1 : t.u0;
     const int sh = (qq & 2) ? 8 : 0;
@@ -226,6 +250,10 @@ __device__ __forceinline__ void load_sub_plain(const PlanePtrs& P, int K, int n,
   if constexpr (QT == QT_Q4_K) {
     r.q = *(const u32x4_t*)(P.p[0] + s * 16);
     h.h = *(const u32x4_t*)(P.p[1] + g * 16);
+  } else if constexpr (QT == QT_Q5_K) {
+    r.q = *(const u32x4_t*)(P.p[0] + s * 16);
+    r.qh = *(const uint32_t*)(P.p[1] + s * 4);
+    h.h = *(const u32x4_t*)(P.p[2] + g * 16);
   } else if constexpr (QT == QT_Q4_0) {
     r.q = *(const u32x4_t*)(P.p[0] + s * 16);
     r.d = *(const uint16_t*)(P.p[1] + s * 2);

@@ -91,7 +91,8 @@ int mlxr_synth_gguf(int qtype, int N, int K, uint64_t seed, void* out_host) {
   int rc = mlxr_qgemm_gguf_size(qtype, N, K, &bytes);
   if (rc) return rc;
   if (!out_host) return MLXR_E_INVALID;
-  if (qtype != MLXR_Q8_0 && qtype != MLXR_Q4_K && qtype != MLXR_Q6_K && qtype != MLXR_Q4_0 && qtype != MLXR_Q4_1)
+  if (qtype != MLXR_Q8_0 && qtype != MLXR_Q4_K && qtype != MLXR_Q6_K && qtype != MLXR_Q4_0 && qtype != MLXR_Q4_1 &&
+      qtype != MLXR_Q5_K)
     return MLXR_E_UNSUPPORTED;
   const int g = mlxr_qgemm_group_size(qtype);
   if (K % g) return MLXR_E_SHAPE;
@@ -112,6 +113,13 @@ int mlxr_synth_gguf(int qtype, int N, int K, uint64_t seed, void* out_host) {
       put16(p + 2, f32_to_f16((float)(r.normal() * 8e-3)));
       fill_bytes(r, p + 4, 16);
       p += 20;
+    } else if (qtype == MLXR_Q5_K) {
+      put16(p, f32_to_f16((float)(fabs(r.normal()) * 1e-3)));
+      put16(p + 2, f32_to_f16((float)(fabs(r.normal()) * 1e-3)));
+      fill_bytes(r, p + 4, 12);   // scales
+      fill_bytes(r, p + 16, 32);  // qh
+      fill_bytes(r, p + 48, 128); // qs
+      p += 176;
     } else if (qtype == MLXR_Q4_K) {
       put16(p, f32_to_f16((float)(fabs(r.normal()) * 1e-3)));
       put16(p + 2, f32_to_f16((float)(fabs(r.normal()) * 1e-3)));

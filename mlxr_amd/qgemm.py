@@ -127,7 +127,7 @@ def quant_type_name(qtype):
 
 
 _BPW = {QuantType.Q4_0: 18 / 32, QuantType.Q4_1: 20 / 32, QuantType.Q8_0: 34 / 32,
-        QuantType.Q4_K: 144 / 256, QuantType.Q6_K: 210 / 256}
+        QuantType.Q4_K: 144 / 256, QuantType.Q5_K: 176 / 256, QuantType.Q6_K: 210 / 256}
 
 
 def get_bytes_per_weight(qtype):

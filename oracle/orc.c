@@ -14,7 +14,7 @@
  *                                 (q - 8) * d and q * d + m, but in the GGUF element order;
  *                                 the reference's interleaved order is kept as
  *                                 orc_dequant_refcpu_q4 and its relation pinned in tests)
- *   - Q4_K / Q6_K dequant         canonical GGUF block_q4_K / block_q6_K semantics (the
+ *   - Q4_K / Q5_K / Q6_K dequant  canonical GGUF block_q4_K / q5_K / q6_K semantics (the
  *                                 reference's only K-quant routines are the Metal ones at
  *                                 q_gemm_dequant.metal:214-286, which are not GGUF-conformant;
  *                                 the GGUF description is the contract these follow)
@@ -36,7 +36,7 @@
 
 #define QK_K 256
 
-enum { Q4_0 = 0, Q4_1 = 1, Q8_0 = 2, Q4_K = 3, Q6_K = 4 };
+enum { Q4_0 = 0, Q4_1 = 1, Q8_0 = 2, Q4_K = 3, Q6_K = 4, Q5_K = 10 };
 
 /* ---------------------------------------------------------------- fp16/bf16 */
 
@@ -129,7 +129,7 @@ uint16_t orc_f32_to_bf16(float f) {
 int orc_block_elems(int qtype) {
     switch (qtype) {
     case Q4_0: case Q4_1: case Q8_0: return 32;
-    case Q4_K: case Q6_K: return QK_K;
+    case Q4_K: case Q6_K: case Q5_K: return QK_K;
     default: return 0;
     }
 }
@@ -141,6 +141,7 @@ int orc_block_bytes(int qtype) {
     case Q8_0: return 34;
     case Q4_K: return 144;
     case Q6_K: return 210;
+    case Q5_K: return 176;
     default: return 0;
     }
 }
@@ -241,6 +242,31 @@ static void dq_q4_k(const uint8_t* blk, float* y) {
     }
 }
 
+/* block_q5_K = { fp16 d; fp16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]; }
+ * As Q4_K (same 12-byte scale/min packing, same qs nibble order), plus a fifth bit:
+ * element 64c+l (l < 32) takes bit 2c of qh[l], element 64c+32+l bit 2c+1.
+ * w = (d*sc)*q - (dmin*m) with q in 0..31: both products exact, one rounding. */
+static void dq_q5_k(const uint8_t* blk, float* y) {
+    float d = orc_f16_to_f32(rd16(blk));
+    float dmin = orc_f16_to_f32(rd16(blk + 2));
+    const uint8_t* s = blk + 4;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* q = blk + 48;
+    for (int c = 0; c < 4; c++) {
+        int sc0, m0, sc1, m1;
+        orc_q4k_scale_min(s, 2 * c, &sc0, &m0);
+        orc_q4k_scale_min(s, 2 * c + 1, &sc1, &m1);
+        float d0 = d * (float)sc0, mm0 = dmin * (float)m0;
+        float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+        for (int l = 0; l < 32; l++) {
+            int lo = (q[32 * c + l] & 0x0f) | (((qh[l] >> (2 * c)) & 1) << 4);
+            int hi = (q[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4);
+            y[64 * c + l] = d0 * (float)lo - mm0;
+            y[64 * c + 32 + l] = d1 * (float)hi - mm1;
+        }
+    }
+}
+
 /* block_q6_K = { u8 ql[128]; u8 qh[64]; int8 scales[16]; fp16 d; }
  * Two 128-element halves; in half h, for l in 0..31 and quarter t in 0..3 the
  * element 128h+32t+l takes its low 4 bits from ql[64h + l + 32(t&1)] (low nibble
@@ -285,6 +311,7 @@ int orc_dequant(int qtype, int N, int K, const uint8_t* w, float* out) {
             else if (qtype == Q4_0) dq_q4_0(blk, y);
             else if (qtype == Q4_1) dq_q4_1(blk, y);
             else if (qtype == Q4_K) dq_q4_k(blk, y);
+            else if (qtype == Q5_K) dq_q5_k(blk, y);
             else dq_q6_k(blk, y);
         }
     }

@@ -44,7 +44,8 @@ int main() {
   EXPECT(QGemmDequantPrimitive::get_bytes_per_weight(QuantType::Q6_K) == 210 / 256.0f);
   EXPECT(throws([] { QGemmDequantPrimitive::get_bytes_per_weight(QuantType::Q2_K); }) ==
          "Unsupported quantization type");
-  EXPECT(throws([] { compute_quantized_weight_size(8, 256, QuantType::Q5_K); }) == "Unsupported quantization type");
+  EXPECT(throws([] { compute_quantized_weight_size(8, 256, QuantType::Q3_K); }) == "Unsupported quantization type");
+  EXPECT(compute_quantized_weight_size(4096, 4096, QuantType::Q5_K) == 11534336u);
 
   QGemmDequantPrimitive a(Stream{}, 1, 4096, 4096, QuantType::Q4_K, 256, false);
   QGemmDequantPrimitive b(Stream{}, 1, 4096, 4096, QuantType::Q4_K, 256, false);

@@ -18,7 +18,7 @@ from oracle import orc  # noqa: E402
 
 # (name, qtype, N, K for the dequant blocks, x dtype of the GEMM)
 CASES = [("q8_0", 2, 2, 256, mx.F16), ("q4_k", 3, 4, 1024, mx.BF16), ("q6_k", 4, 4, 1024, mx.BF16),
-         ("q4_0", 0, 4, 256, mx.BF16), ("q4_1", 1, 4, 256, mx.F16)]
+         ("q4_0", 0, 4, 256, mx.BF16), ("q4_1", 1, 4, 256, mx.F16), ("q5_k", 10, 4, 1024, mx.BF16)]
 GEMM_M, GEMM_N, GEMM_K = 3, 256, 512
 
 

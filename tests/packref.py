@@ -15,6 +15,10 @@ def pi_shift(e):
     return 4 * ((e >> 1) + 4 * (e & 1))
 
 
+def q5h_bit(e):
+    return 2 * (e >> 3) + ((e >> 1) & 1) + 8 * (((e >> 2) & 1) + 2 * (e & 1))
+
+
 def q6h_shift(e):
     return 2 * ((e & 7) >> 1) + 16 * (e & 1) + 8 * ((e >> 3) & 1)
 
@@ -58,6 +62,24 @@ def planes(qtype, N, K, gguf):
         nib = np.stack([qs & 15, qs >> 4], axis=3).reshape(N, nsb, 8, 32)  # sub-block 2c, 2c+1
         words = _words_from_nibbles(nib)  # [N, nsb, 8, 4]
         return [words.view(np.uint8).reshape(-1), hdr.reshape(-1)]
+    if qtype == 10:  # Q5_K: Q4_K header and nibbles, fifth bits in q5h_bit order
+        nsb = K // 256
+        b = g.reshape(N, nsb, 176)
+        sc, m = q4k_scale_min(b[..., 4:16])
+        dd = (b[..., 0].astype(np.uint32) | (b[..., 1].astype(np.uint32) << 8)
+              | (b[..., 2].astype(np.uint32) << 16) | (b[..., 3].astype(np.uint32) << 24))
+        hdr = np.zeros((N, nsb, 8), np.uint16)
+        for j in range(8):
+            hdr[..., j] = (sc[..., j] | (m[..., j] << 6) | (((dd >> np.uint32(4 * j)) & 15) << 12)).astype(np.uint16)
+        qh = b[..., 16:48].astype(np.uint32)          # [N, nsb, 32]: bit j of byte l -> sub-block j, elem l
+        qs = b[..., 48:176].reshape(N, nsb, 4, 32)
+        nib = np.stack([qs & 15, qs >> 4], axis=3).reshape(N, nsb, 8, 32)
+        words = _words_from_nibbles(nib)
+        hw = np.zeros((N, nsb, 8), np.uint32)
+        for j in range(8):
+            for e in range(32):
+                hw[..., j] |= ((qh[..., e] >> np.uint32(j)) & 1) << np.uint32(q5h_bit(e))
+        return [words.view(np.uint8).reshape(-1), hw.view(np.uint8).reshape(-1), hdr.view(np.uint8).reshape(-1)]
     if qtype == 4:  # Q6_K
         nsb = K // 256
         b = g.reshape(N, nsb, 210)

@@ -48,7 +48,7 @@ def test_metadata_matches_reference_helpers():
     assert mx.gguf_size(mx.QuantType.Q8_0, 2048, 2048) == 4456448
     assert mx.gguf_size(mx.QuantType.Q4_0, 1, 32) == 18  # reference parser test: Q4_0 = 18 B / 32
     assert mx.get_bytes_per_weight(mx.QuantType.Q4_K) < 1.0
-    for qt, N, K in ((3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048), (3, 3, 256), (0, 5, 96), (1, 7, 4096)):
+    for qt, N, K in ((3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048), (3, 3, 256), (0, 5, 96), (1, 7, 4096), (10, 9, 512)):
         ps, gs = mx.packed_size(qt, N, K), mx.gguf_size(qt, N, K)
         assert gs <= ps < gs + 4 * 256  # same bytes, planes 256-byte aligned
 
@@ -61,8 +61,8 @@ def _err(fn):
 
 def test_error_paths():
     L = mx.lib()
-    e = _err(lambda: mx.packed_size(mx.QuantType.Q5_K, 16, 256))
-    assert e.code == -2 and "Unsupported quantization type Q5_K" in str(e)
+    e = _err(lambda: mx.packed_size(mx.QuantType.Q2_K, 16, 256))
+    assert e.code == -2 and "Unsupported quantization type Q2_K" in str(e)
     e = _err(lambda: mx.packed_size(mx.QuantType.Q4_K, 16, 300))
     assert e.code == -3 and "multiple" in str(e)
     e = _err(lambda: mx.packed_size(mx.QuantType.Q6_K, 0, 256))
@@ -84,13 +84,13 @@ def test_error_paths():
 
 def test_last_error_is_thread_local():
     L = mx.lib()
-    assert L.mlxr_qgemm_packed_size(10, 1, 256, ctypes.byref(ctypes.c_size_t())) == -2
+    assert L.mlxr_qgemm_packed_size(8, 1, 256, ctypes.byref(ctypes.c_size_t())) == -2
     seen = []
     t = threading.Thread(target=lambda: seen.append(L.mlxr_qgemm_last_error()))
     t.start()
     t.join()
     assert seen == [b""]
-    assert b"Q5_K" in L.mlxr_qgemm_last_error()
+    assert b"Q2_K" in L.mlxr_qgemm_last_error()
 
 
 def test_python_operator_shape_checks():

@@ -82,7 +82,8 @@ def test_tensor_size_calculation():
     for t, b in {T.F32: 4, T.F16: 2, T.BF16: 2, T.F64: 8, T.I8: 1, T.I16: 2, T.I32: 4, T.I64: 8}.items():
         assert gguf.gguf_block_size(t) == 1 and gguf.type_bytes(t, 5) == 5 * b
     # consistent with the matmul's own size helper for the types it runs
-    for t, qt in ((T.Q4_K, mx.QuantType.Q4_K), (T.Q6_K, mx.QuantType.Q6_K), (T.Q8_0, mx.QuantType.Q8_0)):
+    for t, qt in ((T.Q4_K, mx.QuantType.Q4_K), (T.Q6_K, mx.QuantType.Q6_K), (T.Q8_0, mx.QuantType.Q8_0),
+                  (T.Q5_K, mx.QuantType.Q5_K), (T.Q4_0, mx.QuantType.Q4_0), (T.Q4_1, mx.QuantType.Q4_1)):
         assert gguf.calculate_tensor_size([4096, 1024], t) == mx.gguf_size(qt, 1024, 4096)
     with pytest.raises(mx.QGemmError):
         gguf.type_bytes(T.Q4_K, 100)  # not whole blocks
@@ -100,6 +101,8 @@ def test_type_names():
     assert gguf.quant_type(T.Q4_K) == mx.QuantType.Q4_K
     assert gguf.quant_type(T.Q6_K) == mx.QuantType.Q6_K
     assert gguf.quant_type(T.Q8_0) == mx.QuantType.Q8_0
+    assert gguf.quant_type(T.Q5_K) == mx.QuantType.Q5_K
+    assert gguf.quant_type(T.Q4_0) == mx.QuantType.Q4_0
     with pytest.raises(mx.QGemmError):
         gguf.quant_type(T.F16)
 

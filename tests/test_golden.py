@@ -24,7 +24,8 @@ def _x(g):
 
 
 def test_fixtures_present():
-    assert {os.path.basename(f) for f in FILES} == {"q8_0.npz", "q4_k.npz", "q6_k.npz", "q4_0.npz", "q4_1.npz"}
+    assert {os.path.basename(f) for f in FILES} == {"q8_0.npz", "q4_k.npz", "q6_k.npz", "q4_0.npz", "q4_1.npz",
+                                                        "q5_k.npz"}
 
 
 @pytest.mark.parametrize("f", FILES, ids=os.path.basename)

@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 5e-3
 Q4K, Q6K, Q80 = mx.QuantType.Q4_K, mx.QuantType.Q6_K, mx.QuantType.Q8_0
-Q40, Q41 = mx.QuantType.Q4_0, mx.QuantType.Q4_1
+Q40, Q41, Q5K = mx.QuantType.Q4_0, mx.QuantType.Q4_1, mx.QuantType.Q5_K
 
 
 def _dev_bytes(torch, arr, device):
@@ -36,7 +36,7 @@ def _packed(torch, qt, N, K, seed, device):
 
 
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 64, 1024), (Q6K, 48, 768), (Q80, 40, 2048), (Q4K, 3, 256), (Q40, 33, 96),
-                                    (Q41, 40, 1024)])
+                                    (Q41, 40, 1024), (Q5K, 24, 1280)])
 def test_pack_bytes_match_layout(cuda, qt, N, K):
     import torch
     w = mx.synth_gguf(qt, N, K, 11)
@@ -51,7 +51,7 @@ def test_pack_bytes_match_layout(cuda, qt, N, K):
 
 
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 256, 2048), (Q4K, 1, 256),
-                                    (Q40, 128, 2048), (Q41, 96, 4128)])
+                                    (Q40, 128, 2048), (Q41, 96, 4128), (Q5K, 64, 4096)])
 def test_dequant_f32_bit_exact(cuda, qt, N, K):
     import torch
     w, pw = _packed(torch, qt, N, K, 21, cuda)
@@ -61,7 +61,7 @@ def test_dequant_f32_bit_exact(cuda, qt, N, K):
 
 
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 256, 4096), (Q6K, 128, 8192), (Q80, 64, 2048), (Q40, 64, 1024),
-                                    (Q41, 64, 1056)])
+                                    (Q41, 64, 1056), (Q5K, 32, 2048)])
 def test_dequant_bf16_rne_bit_exact(cuda, qt, N, K):
     import torch
     w, pw = _packed(torch, qt, N, K, 22, cuda)
@@ -77,7 +77,7 @@ GEMV_CASES = [
     (Q6K, 1, 300, 2048), (Q6K, 5, 128, 1280), (Q6K, 64, 64, 512),
     (Q80, 1, 256, 2048), (Q80, 2, 100, 96), (Q80, 40, 64, 1024),
     (Q40, 1, 300, 2048), (Q40, 3, 64, 96), (Q40, 12, 128, 1024), (Q41, 1, 256, 4096), (Q41, 4, 200, 160),
-    (Q41, 64, 64, 512),
+    (Q41, 64, 64, 512), (Q5K, 1, 300, 4096), (Q5K, 3, 64, 768), (Q5K, 20, 128, 512),
 ]
 
 
@@ -103,6 +103,7 @@ MFMA_CASES = [
     (Q41, 5, 64, 160),
     # one wavefront per workgroup (short K) with two M-blocks: every row must be stored
     (Q4K, 40, 64, 256), (Q6K, 64, 32, 512), (Q80, 33, 64, 64),
+    (Q5K, 128, 256, 1024), (Q5K, 9, 96, 768), (Q5K, 300, 200, 2048),
 ]
 
 

@@ -133,7 +133,7 @@ def test_cpp_layers(cuda, tmp_path):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("qt", [mx.QuantType.Q4_K, mx.QuantType.Q6_K, mx.QuantType.Q8_0, mx.QuantType.Q4_0,
-                                mx.QuantType.Q4_1])
+                                mx.QuantType.Q4_1, mx.QuantType.Q5_K])
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 130])
 def test_q_gemm_swiglu_matches_oracle(cuda, qt, M):
     """h = swish(x Wg^T) * (x Wu^T) against fp64 on the oracle's gate and up; one launch for

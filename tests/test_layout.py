@@ -46,6 +46,22 @@ def decode(qt, N, K, planes):
         ds = d[..., None, None] * sc                  # [N, nsb, 8, 2]
         w = np.repeat(ds, 16, axis=-1) * q.astype(np.float32)
         return w.reshape(N, K)
+    if qt == 10:
+        nsb = K // 256
+        q = _nibbles(planes[0].view(np.uint32).reshape(N, nsb, 8, 4))
+        hw = planes[1].view(np.uint32).reshape(N, nsb, 8)
+        for e in range(32):
+            q[..., e] |= ((hw >> np.uint32(packref.q5h_bit(e))) & 1) << 4
+        q = q.astype(np.float32)
+        h = planes[2].view(np.uint16).reshape(N, nsb, 8).astype(np.uint32)
+        dd = np.zeros((N, nsb), np.uint32)
+        for j in range(8):
+            dd |= ((h[..., j] >> 12) & 15) << np.uint32(4 * j)
+        d = (dd & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float32)
+        dmin = (dd >> 16).astype(np.uint16).view(np.float16).astype(np.float32)
+        dsc = (d[..., None] * (h & 63).astype(np.float32))[..., None]
+        dm = (dmin[..., None] * ((h >> 6) & 63).astype(np.float32))[..., None]
+        return (dsc * q - dm).reshape(N, K)
     if qt in (0, 1):
         nb = K // 32
         q = _nibbles(planes[0].view(np.uint32).reshape(N, nb, 4)).astype(np.float32)
@@ -60,7 +76,7 @@ def decode(qt, N, K, planes):
     return (q * d[..., None]).reshape(N, K)
 
 
-@pytest.mark.parametrize("qt,N,K", [(3, 8, 1024), (4, 6, 768), (2, 5, 256), (3, 1, 256), (0, 7, 96), (1, 5, 320)])
+@pytest.mark.parametrize("qt,N,K", [(3, 8, 1024), (4, 6, 768), (2, 5, 256), (3, 1, 256), (0, 7, 96), (1, 5, 320), (10, 6, 768)])
 def test_packed_layout_decodes_to_oracle(qt, N, K):
     w = mx.synth_gguf(qt, N, K, 100 + qt)
     got = decode(qt, N, K, packref.planes(qt, N, K, w))
@@ -68,7 +84,7 @@ def test_packed_layout_decodes_to_oracle(qt, N, K):
 
 
 @pytest.mark.parametrize("qt,N,K", [(3, 14336, 4096), (4, 1024, 8192), (2, 2048, 2048), (0, 4096, 4096),
-                                    (1, 1024, 2080)])
+                                    (1, 1024, 2080), (10, 1024, 4096)])
 def test_packed_size_is_gguf_size(qt, N, K):
     planes = packref.planes(qt, N, K, np.zeros(mx.gguf_size(qt, N, K), np.uint8))
     assert sum(p.size for p in planes) == mx.gguf_size(qt, N, K)

@@ -190,6 +190,58 @@ def test_q4_matches_elementwise_decoder(qt):
     np.testing.assert_array_equal(orc.dequant(qt, N, K, w).view(np.uint32), out.view(np.uint32))
 
 
+# ----------------------------------------------------------------------- Q5_K
+
+def q5k_block(d_bits, dmin_bits, scales, qh, qs):
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([d_bits], np.uint16).view(np.uint8)
+    b[2:4] = np.array([dmin_bits], np.uint16).view(np.uint8)
+    b[4:16] = scales
+    b[16:48] = qh
+    b[48:176] = qs
+    return b
+
+
+_UNIT_SCALES = np.array([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1], np.uint8)  # sc_j = 1, m_j = 0
+
+
+@pytest.mark.parametrize("bit", range(8))
+def test_q5k_single_qh_bit(bit):
+    """qh[l] bit b is the fifth bit of element 32b + l (chunk b/2, high half if b odd)."""
+    for l in (0, 7, 31):
+        qh = np.zeros(32, np.uint8)
+        qh[l] = 1 << bit
+        got = orc.dequant(10, 1, 256, q5k_block(f16(1.0), f16(1.0), _UNIT_SCALES, qh, np.zeros(128, np.uint8)))[0]
+        want = np.zeros(256, np.float32)
+        want[32 * bit + l] = 16.0
+        np.testing.assert_array_equal(got, want)
+
+
+def test_q5k_matches_elementwise_decoder():
+    N, K = 2, 512
+    w = mx.synth_gguf(10, N, K, 71)
+    b = w.reshape(N, K // 256, 176)
+    out = np.empty((N, K), np.float32)
+    for n in range(N):
+        for s in range(K // 256):
+            blk = b[n, s]
+            d = np.float32(blk[0:2].view(np.float16)[0])
+            dmin = np.float32(blk[2:4].view(np.float16)[0])
+            sc = blk[4:16]
+            for e in range(256):
+                c, half, l = e // 64, (e // 32) % 2, e % 32
+                j = 2 * c + half
+                if j < 4:
+                    scj, mj = sc[j] & 63, sc[j + 4] & 63
+                else:
+                    scj = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4)
+                    mj = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4)
+                byte = int(blk[48 + 32 * c + l])
+                q = ((byte >> 4) if half else (byte & 15)) | (((int(blk[16 + l]) >> j) & 1) << 4)
+                out[n, 256 * s + e] = np.float32(np.float64(d * np.float32(scj)) * q - np.float64(dmin * np.float32(mj)))
+    np.testing.assert_array_equal(orc.dequant(10, N, K, w).view(np.uint32), out.view(np.uint32))
+
+
 # ----------------------------------------------------------------------- Q4_K
 
 # One-hot scale bits, derived by hand from the GGUF 12-byte packing: sub-blocks 0..3 keep
@@ -408,5 +460,5 @@ def test_gemm_linearity():
 
 
 def test_unsupported_types_rejected():
-    assert orc.lib().orc_dequant(10, 1, 256, None, None) == -1  # Q5_K has no oracle here
+    assert orc.lib().orc_dequant(8, 1, 256, None, None) == -1  # Q2_K has no oracle here
     assert orc.lib().orc_dequant(Q4K, 1, 300, None, None) == -1  # K not a block multiple
