@@ -62,7 +62,8 @@ enum {
 /* Execution path selector for mlxr_qgemm_run_ex. */
 enum {
   MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M <= 4; MFMA kernels above: skinny (weights
-                         streamed once) for M <= 64, tiled GEMM beyond */
+                         streamed once) for M <= 64, tiled GEMM beyond -- and from M = 17
+                         when mlxr_qgemm_run_ws is given the workspace it asks for */
   MLXR_PATH_GEMV = 1, /* force the wavefront-reduction GEMV kernel (any M <= 64) */
   MLXR_PATH_MFMA = 2  /* force the MFMA kernels (skinny for M <= 64, tiled above) */
 };
@@ -122,16 +123,17 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
                       void* y_dev, int y_dtype, int M, int path, void* stream);
 
 /* Device workspace bytes mlxr_qgemm_run_ws can use for an [M, N, K] problem; 0 when the
- * problem would not use one.  MFMA GEMMs (M > 64) whose output tiles are too few to fill
- * the device split K over several workgroups and add the fp32 partials in a second
- * kernel; the workspace holds those partials (splits x M x N x 4 bytes).  No counterpart
- * in the reference (its kernel has no K split, q_gemm_dequant.metal:374-464). */
+ * problem would not use one.  Tiled MFMA GEMMs (M > 16) whose output tiles are too few to
+ * fill the device split K over several workgroups and add the fp32 partials in a second
+ * kernel; the workspace holds those partials (splits x M x N x 4 bytes).  For 16 < M <= 64
+ * a workspace also moves the call from the skinny kernel to the tiled one (64-row tiles).
+ * No counterpart in the reference (its kernel has no K split, q_gemm_dequant.metal:374-464). */
 int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes);
 
 /* mlxr_qgemm_run_ex with a caller-owned device workspace (workspace_bytes bytes; NULL or
- * too small = no K split, the result of mlxr_qgemm_run_ex).  The workspace must not be
- * in use by other work while this call's kernels run on `stream`.  Split and unsplit
- * results differ only in fp32 summation order; a given (shape, workspace size) always
+ * too small = the kernel and result of mlxr_qgemm_run_ex).  The workspace must not be
+ * in use by other work while this call's kernels run on `stream`.  The two choices differ
+ * only in fp32 summation order; a given (shape, workspace size) always
  * takes the same choice, so repeated calls are bit-identical. */
 int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packed_dev,
                       const void* x_dev, int x_dtype, const void* bias_dev, int bias_dtype,

@@ -6,6 +6,7 @@
 // no exception crosses the C ABI.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <string>
 #include <vector>
@@ -17,6 +18,10 @@ namespace {
 
 // Largest M the automatic path sends to the GEMV kernel.
 constexpr int kGemvMaxM = 4;
+// Above this M (and up to 64) the tiled GEMM with 64-row tiles and split-K beats the
+// skinny kernel when the caller provides a workspace (measured on MI355X, Llama-3-8B FFN
+// shapes: M = 32 down 35.4 vs 45.6 us, M = 64 gate 30.1 vs 42.7 us).
+constexpr int kSkinnyOnlyMaxM = 16;
 
 thread_local std::string g_err;
 
@@ -162,7 +167,7 @@ int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes) {
   if (rc) return rc;
   if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
   if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
-  *bytes = M > 64 ? mlxr::mfma_workspace_bytes(M, N, K) : 0;
+  *bytes = M > kSkinnyOnlyMaxM ? mlxr::mfma_workspace_bytes(M, N, K) : 0;
   return MLXR_OK;
 }
 
@@ -203,11 +208,17 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   a.ws = workspace_dev;
   a.ws_bytes = workspace_dev ? workspace_bytes : 0;
   // GEMV (no MFMA) for decode; MFMA kernels otherwise: the skinny one up to M = 64, the
-  // tiled one above (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
+  // tiled one above -- and from M = 17 when a workspace lets it split K
+  // (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
   const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= kGemvMaxM);
+  bool skinny = false;
+  if (!gemv && M <= 64) {
+    const size_t need = M > kSkinnyOnlyMaxM ? mlxr::mfma_workspace_bytes(M, a.L.N, a.L.K) : 0;
+    skinny = need == 0 || !a.ws || a.ws_bytes < need;
+  }
   hipError_t e;
   if (gemv) e = mlxr::launch_gemv(a, (hipStream_t)stream);
-  else if (M <= 64) e = mlxr::launch_skinny(a, (hipStream_t)stream);
+  else if (skinny) e = mlxr::launch_skinny(a, (hipStream_t)stream);
   else e = mlxr::launch_mfma(a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, gemv ? "gemv launch" : "mfma launch");
   return MLXR_OK;

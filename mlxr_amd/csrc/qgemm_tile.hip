@@ -381,7 +381,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
 
 template <int QT, int XT, int MI>
 hipError_t launch_tile_t(const TileParams& tp, int nblocks, hipStream_t s) {
-  constexpr int lds_bytes = NSTAGE * 32 * MI * TK * 2;
+  // activation stages, or the epilogue's four 32 x 68 fp32 blocks if larger (MI = 2)
+  constexpr int lds_bytes = std::max(NSTAGE * 32 * MI * TK * 2, 4 * 32 * 68 * 4);
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute((const void*)qgemm_tile_kernel<QT, XT, MI>,
@@ -418,8 +419,8 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
   const long tn = (N + TN - 1) / TN;
   SplitPlan best{256, 0, 1, 0};
   double best_t = 1e30;
-  for (int bm : {256, 128}) {
-    if ((force_bm == 128 || force_bm == 256) && bm != force_bm) continue;
+  for (int bm : {256, 128, 64}) {
+    if ((force_bm == 64 || force_bm == 128 || force_bm == 256) && bm != force_bm) continue;
     const long tiles = ((M + bm - 1) / bm) * tn;
     for (int S = 1; S <= 8; ++S) {
       if (force_s >= 1 && S != std::min(force_s, (nkt + 3) / 4)) continue;
@@ -428,7 +429,7 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
       if (Sr != S) continue;
       if (S > 1 && ((force_s < 1 && kps < 8) || (size_t)S * (size_t)M * (size_t)N * 4u > ws_bytes)) continue;
       const long rounds = (tiles * S + cus - 1) / cus;
-      double t = (double)rounds * (kps * (bm == 256 ? 1.0 : 0.64) + 0.8);
+      double t = (double)rounds * (kps * (bm == 256 ? 1.0 : bm == 128 ? 0.64 : 0.5) + 0.8);
       if (S > 1) t += (3.0 + (double)S * M * N * 8.0 / 5e6) / 1.86;
       if (t < best_t) {
         best_t = t;
@@ -437,7 +438,7 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
     }
   }
   if (best.kps == 0) {  // nothing qualified (a forced split without workspace): no split
-    best.bm = force_bm == 128 ? 128 : 256;
+    best.bm = (force_bm == 64 || force_bm == 128) ? force_bm : 256;
     best.tiles = (int)(((M + best.bm - 1) / best.bm) * tn);
     best.S = 1;
     best.kps = nkt;
@@ -450,6 +451,7 @@ hipError_t launch_q(TileParams tp, int bm, int S, hipStream_t s) {
   tp.tiles_m = (tp.M + bm - 1) / bm;
   tp.tiles_n = (tp.N + TN - 1) / TN;
   const int ntiles = tp.tiles_m * tp.tiles_n;
+  if (bm == 64) return launch_tile_t<QT, XT, 2>(tp, ntiles * S, s);
   return bm == 128 ? launch_tile_t<QT, XT, 4>(tp, ntiles * S, s) : launch_tile_t<QT, XT, 8>(tp, ntiles * S, s);
 }
 
@@ -593,7 +595,7 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
 }
 
 size_t mfma_workspace_bytes(int M, int N, int K) {
-  if (M <= 64 || (size_t)M * (size_t)K * 2u >= ((size_t)1 << 31)) return 0;
+  if ((size_t)M * (size_t)K * 2u >= ((size_t)1 << 31)) return 0;
   const SplitPlan sp = plan_split(M, N, K, ~(size_t)0);
   return sp.S > 1 ? (size_t)sp.S * (size_t)M * (size_t)N * 4u : 0;
 }
