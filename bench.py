@@ -307,6 +307,16 @@ def run_c4(cx, args):
             tot_us += us
         res[f"M={M}"] = {"TFLOPs": round(tot_f / tot_us / 1e6, 1),
                          "frac_bf16_peak": round(tot_f / tot_us / 1e6 / BF16_PEAK_TFLOPS, 4), "shapes": shapes}
+    # context only: a plain (unquantized) bf16 GEMM of the same gate shape through torch's
+    # library path (hipBLASLt), i.e. what the MFMA units give without any dequant work
+    M, N, K = 2048, 14336, 4096
+    a = cx.act(M, K, mx.BF16, SEED_BASE + 4200)
+    b = torch.randn((N, K), dtype=torch.bfloat16, device=cx.dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev)
+    fn = lambda r: torch.matmul(a, b.t(), out=y)
+    fn(0)
+    us = 1e3 * cx.graph_ms(fn, 5)
+    res["plain_bf16_gemm_library_M2048_gate"] = {"us": round(us, 1), "TFLOPs": round(2.0 * M * N * K / us / 1e6, 1)}
     return res
 
 
