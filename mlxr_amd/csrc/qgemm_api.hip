@@ -167,7 +167,9 @@ int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes) {
   if (rc) return rc;
   if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
   if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
-  *bytes = M > kSkinnyOnlyMaxM ? mlxr::mfma_workspace_bytes(M, N, K) : 0;
+  *bytes = M > kSkinnyOnlyMaxM ? mlxr::mfma_workspace_bytes(M, N, K)
+          : M > kGemvMaxM      ? mlxr::skinny_workspace_bytes(M, N, K, qtype)
+                               : 0;
   return MLXR_OK;
 }
 

@@ -56,7 +56,13 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s);
 // Workspace bytes launch_mfma would use for an [M, N, K] problem (0: no split).
 size_t mfma_workspace_bytes(int M, int N, int K);
 
-// Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.
+// Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.  With a.ws,
+// shapes with fewer 32-row slabs than CUs also split K over workgroups.
 hipError_t launch_skinny(const RunArgs& a, hipStream_t s);
+// Workspace bytes launch_skinny would use (0: no split).
+size_t skinny_workspace_bytes(int M, int N, int K, int qtype);
+// y = sum of S fp32 partial planes (split order) + bias, converted (qgemm_tile.hip).
+hipError_t launch_splitk_reduce(const float* ws, size_t split_elems, int S, const void* bias, int bias_dtype, void* y,
+                                int y_dtype, int M, int N, hipStream_t s);
 
 }  // namespace mlxr

@@ -51,6 +51,10 @@ struct SkinnyParams {
   int M, N, K;
   int bias_dtype, y_dtype;
   int spw;  // K steps per wavefront (multiple of RING)
+  int slabs;        // 32-row slabs; the grid is slabs x K splits
+  int spg;          // K steps per workgroup (multiple of RING)
+  float* ws;        // K splits over workgroups: fp32 partials, split s at ws + s * ws_split
+  size_t ws_split;  // elements per split plane
   uint32_t nib;
 };
 
@@ -84,11 +88,13 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
   const int M = p.M, N = p.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK - 1) / TK;
-  const int n0 = blockIdx.x * 32;
+  const int ksplit = blockIdx.x / p.slabs;
+  const int n0 = (blockIdx.x - ksplit * p.slabs) * 32;
   const int h = lane >> 5, n = n0 + (lane & 31);
   const bool rok = n < N;
   const uint32_t row_sub = rok ? (uint32_t)n * (uint32_t)nsub : 0u, row_sb = rok ? (uint32_t)n * (uint32_t)nsb : 0u;
-  const int kt0 = wave * p.spw, kt1 = min(nkt, kt0 + p.spw);
+  const int kg1 = min(nkt, (ksplit + 1) * p.spg);
+  const int kt0 = ksplit * p.spg + wave * p.spw, kt1 = min(kg1, kt0 + p.spw);
   rsrc_t R[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, p.psize[i]);
@@ -190,6 +196,21 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
       out[v] = s;
     }
     const size_t rowbase = (size_t)m * N;
+    if (p.ws) {  // K split over workgroups: this split's fp32 partial sums, no bias
+      float* wsp = p.ws + (size_t)ksplit * p.ws_split + rowbase;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nn = n0 + 8 * q + 4 * (lane >> 5);
+        if ((N & 3) == 0 && nn + 3 < N) {
+          *(float4*)(wsp + nn) = make_float4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (nn + e < N) wsp[nn + e] = out[4 * q + e];
+        }
+      }
+      continue;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int nn = n0 + 8 * q + 4 * (lane >> 5);
@@ -224,23 +245,47 @@ int device_cus_s() {
   return cus;
 }
 
-template <int QT, int XT>
-hipError_t launch_s(SkinnyParams sp, hipStream_t s) {
-  const int slabs = (sp.N + 31) / 32;
-  const int nkt = (sp.K + TK - 1) / TK;
-  // wavefronts per slab: enough for about eight per CU, at most MAXW; each takes a whole
-  // number of rings of steps, so the ranges start on super-block boundaries
+// Launch geometry: workgroups own 32-row slabs and, when the slabs are fewer than the CUs
+// and a workspace is allowed, a K range (ks splits, each a whole number of rings); inside
+// a workgroup the wavefronts split the range again, enough of them for about eight per CU.
+struct SkinnyPlan {
+  int ks, spg, w, spw;
+};
+SkinnyPlan skinny_plan(int N, int K, int ring, bool allow_split) {
   static const int wpc = getenv("MLXR_SKINNY_WPC") ? atoi(getenv("MLXR_SKINNY_WPC")) : 8;
-  const long want = (long)wpc * device_cus_s();
-  int w = (int)std::min<long>(MAXW, std::max<long>(1, (want + slabs - 1) / slabs));
+  const int cus = device_cus_s();
+  const int slabs = (N + 31) / 32;
+  const int nkt = (K + TK - 1) / TK;
+  SkinnyPlan pl;
+  pl.ks = allow_split && slabs < cus ? std::max(1, std::min(cus / slabs, nkt / ring)) : 1;
+  pl.spg = (((nkt + pl.ks - 1) / pl.ks) + ring - 1) / ring * ring;
+  pl.ks = (nkt + pl.spg - 1) / pl.spg;
+  const long want = (long)wpc * cus;
+  pl.w = (int)std::min<long>(MAXW, std::max<long>(1, (want + (long)slabs * pl.ks - 1) / ((long)slabs * pl.ks)));
+  pl.spw = (((pl.spg + pl.w - 1) / pl.w) + ring - 1) / ring * ring;
+  pl.w = (pl.spg + pl.spw - 1) / pl.spw;
+  return pl;
+}
+
+template <int QT, int XT>
+hipError_t launch_s(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   constexpr int RING = ring_steps<QT>();
-  int spw = (((nkt + w - 1) / w) + RING - 1) / RING * RING;
-  w = (nkt + spw - 1) / spw;
-  sp.spw = spw;
-  const dim3 grid((unsigned)slabs), block((unsigned)(64 * w));
+  sp.slabs = (sp.N + 31) / 32;
+  SkinnyPlan pl = skinny_plan(sp.N, sp.K, RING, sp.ws != nullptr);
+  if (pl.ks > 1 && (size_t)pl.ks * (size_t)sp.M * (size_t)sp.N * 4u > ws_bytes) pl = skinny_plan(sp.N, sp.K, RING, false);
+  sp.spg = pl.spg;
+  sp.spw = pl.spw;
+  sp.ws_split = (size_t)sp.M * (size_t)sp.N;
+  float* const ws = (float*)sp.ws;
+  void* const y = sp.y;
+  const void* const bias = sp.bias;
+  if (pl.ks == 1) sp.ws = nullptr;
+  const dim3 grid((unsigned)(sp.slabs * pl.ks)), block((unsigned)(64 * pl.w));
   if (sp.M <= 32) qgemm_skinny_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
   else qgemm_skinny_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);
-  return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || pl.ks == 1) return e;
+  return launch_splitk_reduce(ws, sp.ws_split, pl.ks, bias, sp.bias_dtype, y, sp.y_dtype, sp.M, sp.N, s);
 }
 
 }  // namespace
@@ -258,15 +303,22 @@ hipError_t launch_skinny(const RunArgs& a, hipStream_t s) {
   sp.bias_dtype = a.bias_dtype;
   sp.y_dtype = a.y_dtype;
   sp.nib = 0x0F0F0F0Fu;
+  sp.ws = (float*)a.ws;
+  const size_t wsb = a.ws ? a.ws_bytes : 0;
   const bool f16 = a.x_dtype == DT_F16;
   switch (a.L.qtype) {
-    case QT_Q4_K: return f16 ? launch_s<QT_Q4_K, X_F16>(sp, s) : launch_s<QT_Q4_K, X_BF16>(sp, s);
-    case QT_Q6_K: return f16 ? launch_s<QT_Q6_K, X_F16>(sp, s) : launch_s<QT_Q6_K, X_BF16>(sp, s);
-    case QT_Q5_K: return f16 ? launch_s<QT_Q5_K, X_F16>(sp, s) : launch_s<QT_Q5_K, X_BF16>(sp, s);
-    case QT_Q4_0: return f16 ? launch_s<QT_Q4_0, X_F16>(sp, s) : launch_s<QT_Q4_0, X_BF16>(sp, s);
-    case QT_Q4_1: return f16 ? launch_s<QT_Q4_1, X_F16>(sp, s) : launch_s<QT_Q4_1, X_BF16>(sp, s);
-    default: return f16 ? launch_s<QT_Q8_0, X_F16>(sp, s) : launch_s<QT_Q8_0, X_BF16>(sp, s);
+    case QT_Q4_K: return f16 ? launch_s<QT_Q4_K, X_F16>(sp, wsb, s) : launch_s<QT_Q4_K, X_BF16>(sp, wsb, s);
+    case QT_Q6_K: return f16 ? launch_s<QT_Q6_K, X_F16>(sp, wsb, s) : launch_s<QT_Q6_K, X_BF16>(sp, wsb, s);
+    case QT_Q5_K: return f16 ? launch_s<QT_Q5_K, X_F16>(sp, wsb, s) : launch_s<QT_Q5_K, X_BF16>(sp, wsb, s);
+    case QT_Q4_0: return f16 ? launch_s<QT_Q4_0, X_F16>(sp, wsb, s) : launch_s<QT_Q4_0, X_BF16>(sp, wsb, s);
+    case QT_Q4_1: return f16 ? launch_s<QT_Q4_1, X_F16>(sp, wsb, s) : launch_s<QT_Q4_1, X_BF16>(sp, wsb, s);
+    default: return f16 ? launch_s<QT_Q8_0, X_F16>(sp, wsb, s) : launch_s<QT_Q8_0, X_BF16>(sp, wsb, s);
   }
+}
+
+size_t skinny_workspace_bytes(int M, int N, int K, int qtype) {
+  const SkinnyPlan pl = skinny_plan(N, K, qtype == QT_Q8_0 ? 4 : 8, true);
+  return pl.ks > 1 ? (size_t)pl.ks * (size_t)M * (size_t)N * 4u : 0;
 }
 
 }  // namespace mlxr

@@ -555,16 +555,8 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
     tp.ws_split = (size_t)M * (size_t)N;
     hipError_t e = launch_chunk(tp, sp.bm, sp.S, a.L.qtype, a.x_dtype == DT_F16, s);
     if (e != hipSuccess) return e;
-    const size_t total = (size_t)M * (size_t)N;
-    if ((N & 3) == 0) {
-      const size_t threads = total / 4;
-      splitk_reduce_kernel<4><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(
-          (const float*)a.ws, tp.ws_split, sp.S, a.bias, a.bias_dtype, a.y, a.y_dtype, N, total);
-    } else {
-      splitk_reduce_kernel<1><<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
-          (const float*)a.ws, tp.ws_split, sp.S, a.bias, a.bias_dtype, a.y, a.y_dtype, N, total);
-    }
-    return hipGetLastError();
+    return launch_splitk_reduce((const float*)a.ws, tp.ws_split, sp.S, a.bias, a.bias_dtype, a.y, a.y_dtype, M, N,
+                                s);
   }
   for (int mc = 0; mc < M; mc += Mc) {
     for (int nc = 0; nc < N; nc += Nc) {
@@ -598,6 +590,20 @@ size_t mfma_workspace_bytes(int M, int N, int K) {
   if ((size_t)M * (size_t)K * 2u >= ((size_t)1 << 31)) return 0;
   const SplitPlan sp = plan_split(M, N, K, ~(size_t)0);
   return sp.S > 1 ? (size_t)sp.S * (size_t)M * (size_t)N * 4u : 0;
+}
+
+hipError_t launch_splitk_reduce(const float* ws, size_t split_elems, int S, const void* bias, int bias_dtype, void* y,
+                                int y_dtype, int M, int N, hipStream_t s) {
+  const size_t total = (size_t)M * (size_t)N;
+  if ((N & 3) == 0) {
+    const size_t threads = total / 4;
+    splitk_reduce_kernel<4><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s>>>(
+        ws, split_elems, S, bias, bias_dtype, y, y_dtype, N, total);
+  } else {
+    splitk_reduce_kernel<1><<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
+        ws, split_elems, S, bias, bias_dtype, y, y_dtype, N, total);
+  }
+  return hipGetLastError();
 }
 
 }  // namespace mlxr

@@ -242,11 +242,14 @@ def test_mfma_chunked_launches(cuda, monkeypatch):
 @pytest.mark.parametrize("qt,M,N,K,ydt", [(Q4K, 512, 1024, 4096, "bf16"), (Q6K, 256, 1000, 2048, "f32"),
                                           (Q41, 300, 512, 4096, "bf16"), (Q4K, 40, 1024, 4096, "bf16"),
                                           (Q6K, 64, 512, 2048, "f32"), (Q5K, 17, 768, 1024, "f16"),
+                                          (Q4K, 8, 1024, 8192, "bf16"), (Q6K, 12, 2048, 4096, "f32"),
+                                          (Q80, 5, 512, 2048, "f16"), (Q41, 16, 992, 4096, "bf16"),
                                           (Q80, 130, 384, 1056, "f16"), (Q4K, 2048, 1024, 4096, "f32")])
 def test_mfma_split_k(cuda, qt, M, N, K, ydt):
     """Split-K through the C ABI: mlxr_qgemm_run_ws with the workspace size the library
-    asks for splits K (partials + reduce kernel; for 16 < M <= 64 the tiled kernel with
-    64-row tiles instead of the skinny one) and stays within tolerance of the oracle,
+    asks for splits K over workgroups (partials + reduce kernel: the skinny kernel for
+    M <= 16 with fewer 32-row slabs than CUs, the tiled kernel otherwise, with 64-row tiles
+    for 16 < M <= 64) and stays within tolerance of the oracle,
     with bias, for every output dtype and N % 4 != 0; repeated calls are bit-identical, and
     a workspace one byte too small gives exactly the unsplit mlxr_qgemm_run_ex result."""
     import ctypes
