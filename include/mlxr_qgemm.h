@@ -62,7 +62,7 @@ enum {
 /* Execution path selector for mlxr_qgemm_run_ex. */
 enum {
   MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M <= 4; MFMA kernels above: skinny (weights
-                         streamed once) for M <= 64, tiled GEMM beyond -- and from M = 17
+                         streamed once) for M <= 64, tiled GEMM beyond -- and from M = 33
                          when mlxr_qgemm_run_ws is given the workspace it asks for */
   MLXR_PATH_GEMV = 1, /* force the wavefront-reduction GEMV kernel (any M <= 64) */
   MLXR_PATH_MFMA = 2  /* force the MFMA kernels (skinny for M <= 64, tiled above) */
@@ -123,10 +123,11 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
                       void* y_dev, int y_dtype, int M, int path, void* stream);
 
 /* Device workspace bytes mlxr_qgemm_run_ws can use for an [M, N, K] problem; 0 when the
- * problem would not use one.  Tiled MFMA GEMMs (M > 16) whose output tiles are too few to
- * fill the device split K over several workgroups and add the fp32 partials in a second
- * kernel; the workspace holds those partials (splits x M x N x 4 bytes).  For 16 < M <= 64
- * a workspace also moves the call from the skinny kernel to the tiled one (64-row tiles).
+ * problem would not use one.  MFMA GEMMs whose workgroups would be too few to fill the
+ * device (tiled ones, M > 32, and skinny ones with few 32-row slabs) split K over several
+ * workgroups and add the fp32 partials in a second kernel; the workspace holds those
+ * partials (splits x M x N x 4 bytes).  For 32 < M <= 64 a workspace also moves the call
+ * from the skinny kernel to the tiled one (64-row tiles).
  * No counterpart in the reference (its kernel has no K split, q_gemm_dequant.metal:374-464). */
 int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes);
 

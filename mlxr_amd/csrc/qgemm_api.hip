@@ -20,8 +20,13 @@ namespace {
 constexpr int kGemvMaxM = 4;
 // Above this M (and up to 64) the tiled GEMM with 64-row tiles and split-K beats the
 // skinny kernel when the caller provides a workspace (measured on MI355X, Llama-3-8B FFN
-// shapes: M = 32 down 35.4 vs 45.6 us, M = 64 gate 30.1 vs 42.7 us).
-constexpr int kSkinnyOnlyMaxM = 16;
+// shapes: at M = 32 the skinny kernel's 16x16x32 variant is ahead, gate 26.9 vs 29.0 us
+// and down 26.7 vs 29.7 us; at M = 64 the tiled one, gate 28.3 vs 42.7 us).
+constexpr int kSkinnyOnlyMaxM = 32;
+int skinny_only_max_m() {  // MLXR_SKINNY_ONLY_MAX_M overrides (tuning)
+  static const int v = getenv("MLXR_SKINNY_ONLY_MAX_M") ? atoi(getenv("MLXR_SKINNY_ONLY_MAX_M")) : kSkinnyOnlyMaxM;
+  return v;
+}
 
 thread_local std::string g_err;
 
@@ -167,7 +172,7 @@ int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes) {
   if (rc) return rc;
   if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
   if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
-  *bytes = M > kSkinnyOnlyMaxM ? mlxr::mfma_workspace_bytes(M, N, K)
+  *bytes = M > skinny_only_max_m() ? mlxr::mfma_workspace_bytes(M, N, K)
           : M > kGemvMaxM      ? mlxr::skinny_workspace_bytes(M, N, K, qtype)
                                : 0;
   return MLXR_OK;
@@ -210,12 +215,12 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   a.ws = workspace_dev;
   a.ws_bytes = workspace_dev ? workspace_bytes : 0;
   // GEMV (no MFMA) for decode; MFMA kernels otherwise: the skinny one up to M = 64, the
-  // tiled one above -- and from M = 17 when a workspace lets it split K
+  // tiled one above -- and from M = 33 when a workspace lets it split K
   // (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
   const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= kGemvMaxM);
   bool skinny = false;
   if (!gemv && M <= 64) {
-    const size_t need = M > kSkinnyOnlyMaxM ? mlxr::mfma_workspace_bytes(M, a.L.N, a.L.K) : 0;
+    const size_t need = M > skinny_only_max_m() ? mlxr::mfma_workspace_bytes(M, a.L.N, a.L.K) : 0;
     skinny = need == 0 || !a.ws || a.ws_bytes < need;
   }
   hipError_t e;

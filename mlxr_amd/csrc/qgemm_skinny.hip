@@ -233,6 +233,216 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Narrow variant for M <= 32 on the 16x16x32 MFMA.  The activations are the second
+// operand in 16-row blocks (NB of them), so at M = 8 or 16 half or none of the operand is
+// padding instead of the 24 or 16 of 32 rows above, and each activation load feeds twice
+// the weights: a step is 128 of K, a lane (r, j) = (lane % 16, lane / 16) owns sub-block j
+// of the step for weight rows n0 + r and n0 + 16 + r, and MFMA kk takes word kk of every
+// lane's sub-block (K positions 32j + 8kk .. +7 of the step, for both operands).  A
+// K-quant super-block spans two steps: the lane's sub-blocks are j and 4 + j of it.
+// Partial tiles of the workgroup's wavefronts meet in LDS as above.
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+constexpr int TK16 = 128;
+template <int QT>
+constexpr int ring16_steps() { return QT == QT_Q8_0 ? 2 : 4; }
+constexpr int UNROLL16 = 4;  // steps per loop trip; steps per wavefront are a multiple
+
+template <int XT>
+__device__ __forceinline__ f32x4_t mfma16(const uint4& a, const u32x4_t& b, const f32x4_t& c) {
+  if constexpr (XT == X_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+}
+
+// Factors of sub-blocks j and 4 + j of a super-block (slots 0 and 1 of Scales): header
+// entry e sits in word e / 2, half e % 2 (the layout decode_hdr reads).
+template <int QT>
+__device__ __forceinline__ void decode_hdr16(const Hdr<QT>& h, int j, Scales<QT>& s) {
+  const uint32_t w[4] = {h.h[0], h.h[1], h.h[2], h.h[3]};
+  if constexpr (QT == QT_Q4_K || QT == QT_Q5_K) {
+    const uint32_t dd = q4k_dd(make_uint4(w[0], w[1], w[2], w[3]));
+    const float d = f16_bits_to_f32(dd & 0xffffu), dmin = f16_bits_to_f32(dd >> 16);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t v = w[2 * q + (j >> 1)];
+      const uint32_t f = ((j & 1) ? (v >> 16) : v) & 0xfffu;
+      s.a[q] = d * (float)(f & 63u);
+      s.b[q] = -(dmin * (float)(f >> 6));
+    }
+  } else if constexpr (QT == QT_Q6_K) {
+    const float d = f16_bits_to_f32(h.d & 0xffffu);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t v0 = w[2 * q + (j >> 1)];
+      const uint32_t v = (j & 1) ? (v0 >> 16) : v0;
+      s.a[q] = d * (float)(int8_t)(v & 0xffu);
+      s.b[q] = d * (float)(int8_t)((v >> 8) & 0xffu);
+    }
+  }
+}
+
+template <int QT, int XT, int NB>
+__global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams p) {
+  constexpr int D = ring16_steps<QT>();  // raw ring; loads run D - 1 steps ahead
+  constexpr int RT = 2;                  // 16-row weight tiles per wavefront
+  constexpr bool KQ = is_kquant(QT);
+  constexpr int XD = 2;                  // activation loads run two steps ahead
+  __shared__ f32x4_t red[MAXW][RT * NB][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = blockDim.x >> 6;
+  const int M = p.M, N = p.N, K = p.K;
+  const int nsub = K >> 5, nsb = K >> 8;
+  const int nkt = (K + TK16 - 1) / TK16;
+  const int ksplit = blockIdx.x / p.slabs;
+  const int n0 = (blockIdx.x - ksplit * p.slabs) * 32;
+  const int r = lane & 15, j = lane >> 4;
+  uint32_t row_sub[RT], row_sb[RT];
+  bool rok[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int n = n0 + 16 * t + r;
+    rok[t] = n < N;
+    row_sub[t] = rok[t] ? (uint32_t)n * (uint32_t)nsub : 0u;
+    row_sb[t] = rok[t] ? (uint32_t)n * (uint32_t)nsb : 0u;
+  }
+  const int kg1 = min(nkt, (ksplit + 1) * p.spg);
+  const int kt0 = ksplit * p.spg + wave * p.spw, kt1 = min(kg1, kt0 + p.spw);
+  rsrc_t R[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, p.psize[i]);
+  const rsrc_t RX = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+
+  // activations: lane (m, j) of block nb reads row nb*16 + m, K 32j .. 32j+31 of the step
+  uint32_t xoff[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int m = nb * 16 + r;
+    xoff[nb] = m < M ? ((uint32_t)m * (uint32_t)K + 32u * (uint32_t)j) * 2u : OOB;
+  }
+  u32x4_t xf[4][4][NB];  // step s in slot s % 4 (three live: loads run two steps ahead)
+  auto load_x = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+    const bool live = kt < kt1 && 4 * kt + j < nsub;
+    const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane(kt * TK16 * 2);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint32_t vo = live ? xoff[nb] : OOB;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) xf[slot][kk][nb] = __builtin_amdgcn_raw_buffer_load_b128(RX, vo + 16 * kk, soff, 0);
+    }
+  };
+
+  Raw<QT> raw[D][RT];
+  Hdr<QT> hdr[KQ ? D / 2 : 1][RT];  // super-block of ring slots 2i, 2i + 1
+  Scales<QT> sc[RT];
+  auto issue_raw = [&](int kt, auto SLOT) {
+    constexpr int slot = decltype(SLOT)::value;
+    const int sb = 4 * kt + j;
+    const bool in = kt < kt1 && sb < nsub;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) load_raw<QT>(R, row_sub[t], sb, in && rok[t], raw[slot][t]);
+    if constexpr (KQ && (slot & 1) == 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) load_hdr<QT>(R, row_sb[t], kt >> 1, in && rok[t], hdr[slot >> 1][t]);
+    }
+  };
+
+  f32x4_t acc[RT][NB];
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  sfor<D - 1>([&](auto S_) {
+    constexpr int s_ = decltype(S_)::value;
+    issue_raw(kt0 + s_, std::integral_constant<int, s_>());
+    if constexpr (s_ < XD) load_x(kt0 + s_, std::integral_constant<int, s_>());
+  });
+  sfor<(XD > D - 1 ? XD - D + 1 : 0)>([&](auto S_) {
+    constexpr int s_ = decltype(S_)::value + D - 1;
+    load_x(kt0 + s_, std::integral_constant<int, s_>());
+  });
+  // Step kt = kt0 + D*i + u (kt0 even, so an even u starts a super-block) issues the raw
+  // loads of step kt + D - 1, then the activations of step kt + 2: the wait for the
+  // activations of step kt (in-order counter) then covers raw loads issued two steps ago.
+  auto step = [&](int kt, auto U) {
+    constexpr int u = decltype(U)::value;
+    issue_raw(kt + D - 1, std::integral_constant<int, (u + D - 1) % D>());
+    load_x(kt + XD, std::integral_constant<int, (u + XD) & 3>());
+    constexpr int ru = u % D;
+    if constexpr (KQ && (u & 1) == 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t) decode_hdr16<QT>(hdr[ru >> 1][t], j, sc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      uint4 w[4];
+      w[0] = dequant_word<QT, XT, 0>(raw[ru][t], sc[t], u & 1, p.nib);
+      w[1] = dequant_word<QT, XT, 1>(raw[ru][t], sc[t], u & 1, p.nib);
+      w[2] = dequant_word<QT, XT, 2>(raw[ru][t], sc[t], u & 1, p.nib);
+      w[3] = dequant_word<QT, XT, 3>(raw[ru][t], sc[t], u & 1, p.nib);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[t][nb] = mfma16<XT>(w[kk], xf[u & 3][kk][nb], acc[t][nb]);
+    }
+  };
+  for (int kt = kt0; kt < kt1; kt += UNROLL16) {
+    sfor<UNROLL16>([&](auto U_) {
+      constexpr int u = decltype(U_)::value;
+      step(kt + u, std::integral_constant<int, u>());
+    });
+  }
+
+  // Accumulator tile (t, nb): lane holds Y[m][n .. n+3] for m = nb*16 + lane%16,
+  // n = n0 + 16t + 4(lane/16).
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) red[wave][t * NB + nb][lane] = acc[t][nb];
+  __syncthreads();
+  for (int u = wave; u < RT * NB; u += nw) {
+    const int t = u / NB, nb = u - t * NB;
+    const int m = nb * 16 + r;
+    if (m >= M) continue;
+    f32x4_t sum = red[0][u][lane];
+    for (int w = 1; w < nw; ++w) sum += red[w][u][lane];
+    const int nn = n0 + 16 * t + 4 * j;
+    const size_t rowbase = (size_t)m * N;
+    if (p.ws) {  // K split over workgroups: this split's fp32 partial sums, no bias
+      float* wsp = p.ws + (size_t)ksplit * p.ws_split + rowbase;
+      if ((N & 3) == 0 && nn + 3 < N) {
+        *(float4*)(wsp + nn) = make_float4(sum[0], sum[1], sum[2], sum[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (nn + e < N) wsp[nn + e] = sum[e];
+      }
+      continue;
+    }
+    float v4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v4[e] = sum[e] + ((p.bias && nn + e < N) ? load_scalar(p.bias, p.bias_dtype, nn + e) : 0.f);
+    if ((N & 3) == 0 && nn + 3 < N && p.y_dtype != DT_F32) {
+      const uint32_t lo = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[0], v4[1]) : pack2<X_F16>(v4[0], v4[1]);
+      const uint32_t hi = p.y_dtype == DT_BF16 ? pack_bf16x2(v4[2], v4[3]) : pack2<X_F16>(v4[2], v4[3]);
+      *(uint2*)((uint16_t*)p.y + rowbase + nn) = make_uint2(lo, hi);
+    } else if ((N & 3) == 0 && nn + 3 < N) {
+      *(float4*)((float*)p.y + rowbase + nn) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nn + e < N) store_scalar(p.y, p.y_dtype, rowbase + nn + e, v4[e]);
+    }
+  }
+}
+
 int device_cus_s() {
   static int cus = 0;
   if (cus == 0) {
@@ -267,8 +477,59 @@ SkinnyPlan skinny_plan(int N, int K, int ring, bool allow_split) {
   return pl;
 }
 
+// The narrow kernels' geometry: as skinny_plan, in 128-wide steps (whole multiples of
+// `unroll` per wavefront), at most `wcap` wavefronts per workgroup, the K split over
+// workgroups sized for about `wpc` wavefronts per CU.
+SkinnyPlan skinny16_plan(int N, int K, bool allow_split, int unroll, int wcap, int wpc) {
+  const int maxw = std::max(1, std::min(wcap, MAXW));
+  const int cus = device_cus_s();
+  const int slabs = (N + 31) / 32;
+  const int nkt = (K + TK16 - 1) / TK16;
+  const long want = (long)wpc * cus;
+  SkinnyPlan pl;
+  pl.ks = 1;
+  // split K over workgroups (partials + a reduce launch, a few us) only when the slabs
+  // alone would fill less than half the target
+  if (allow_split && 2L * slabs * maxw <= want)
+    pl.ks = (int)std::max<long>(1, std::min<long>((want + (long)slabs * maxw - 1) / ((long)slabs * maxw),
+                                                  nkt / unroll));
+  pl.spg = (((nkt + pl.ks - 1) / pl.ks) + unroll - 1) / unroll * unroll;
+  pl.ks = (nkt + pl.spg - 1) / pl.spg;
+  pl.w = (int)std::min<long>(maxw, std::max<long>(1, (want + (long)slabs * pl.ks - 1) / ((long)slabs * pl.ks)));
+  pl.spw = (((pl.spg + pl.w - 1) / pl.w) + unroll - 1) / unroll * unroll;
+  pl.w = (pl.spg + pl.spw - 1) / pl.spw;
+  return pl;
+}
+
+bool use_skinny16(int M) {
+  static const int off = getenv("MLXR_SKINNY16_OFF") ? atoi(getenv("MLXR_SKINNY16_OFF")) : 0;
+  return M <= 32 && !off;
+}
+
+template <int QT, int XT>
+hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
+  sp.slabs = (sp.N + 31) / 32;
+  SkinnyPlan pl = skinny16_plan(sp.N, sp.K, sp.ws != nullptr, UNROLL16, MAXW, 8);
+  if (pl.ks > 1 && (size_t)pl.ks * (size_t)sp.M * (size_t)sp.N * 4u > ws_bytes)
+    pl = skinny16_plan(sp.N, sp.K, false, UNROLL16, MAXW, 8);
+  sp.spg = pl.spg;
+  sp.spw = pl.spw;
+  sp.ws_split = (size_t)sp.M * (size_t)sp.N;
+  float* const ws = (float*)sp.ws;
+  void* const y = sp.y;
+  const void* const bias = sp.bias;
+  if (pl.ks == 1) sp.ws = nullptr;
+  const dim3 grid((unsigned)(sp.slabs * pl.ks)), block((unsigned)(64 * pl.w));
+  if (sp.M <= 16) qgemm_skinny16_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
+  else qgemm_skinny16_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || pl.ks == 1) return e;
+  return launch_splitk_reduce(ws, sp.ws_split, pl.ks, bias, sp.bias_dtype, y, sp.y_dtype, sp.M, sp.N, s);
+}
+
 template <int QT, int XT>
 hipError_t launch_s(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
+  if (use_skinny16(sp.M)) return launch_s16<QT, XT>(sp, ws_bytes, s);
   constexpr int RING = ring_steps<QT>();
   sp.slabs = (sp.N + 31) / 32;
   SkinnyPlan pl = skinny_plan(sp.N, sp.K, RING, sp.ws != nullptr);
@@ -317,7 +578,7 @@ hipError_t launch_skinny(const RunArgs& a, hipStream_t s) {
 }
 
 size_t skinny_workspace_bytes(int M, int N, int K, int qtype) {
-  const SkinnyPlan pl = skinny_plan(N, K, qtype == QT_Q8_0 ? 4 : 8, true);
+  const SkinnyPlan pl = use_skinny16(M) ? skinny16_plan(N, K, true, UNROLL16, MAXW, 8) : skinny_plan(N, K, qtype == QT_Q8_0 ? 4 : 8, true);
   return pl.ks > 1 ? (size_t)pl.ks * (size_t)M * (size_t)N * 4u : 0;
 }
 

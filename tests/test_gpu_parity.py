@@ -239,6 +239,25 @@ def test_mfma_chunked_launches(cuda, monkeypatch):
     assert orc.normwise_rel_err(y1.cpu().numpy(), ref) <= TOL
 
 
+# The skinny kernel's narrow (16x16x32) variant on Q4_K: ragged N, K shorter than or not a
+# multiple of its ring (steps of 128), both activation dtypes, M from 1 to 16.
+@pytest.mark.parametrize("M,N,K,xdt", [(5, 100, 768, mx.BF16), (8, 1000, 2304, mx.F16), (9, 257, 4096, mx.BF16),
+                                       (16, 64, 256, mx.F16), (12, 30, 1280, mx.BF16), (1, 33, 512, mx.BF16),
+                                       (16, 512, 14336, mx.BF16), (7, 4096, 1024, mx.F16)])
+def test_skinny_q4k_matches_oracle(cuda, M, N, K, xdt):
+    import torch
+    w, pw = _packed(torch, Q4K, N, K, 71 + M, cuda)
+    x, xf = _act(torch, M, K, xdt, 81 + N, cuda)
+    y = mx.q_gemm_dequant(x, pw, M, N, K, Q4K, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    ref = orc.gemm_f64(int(Q4K), M, N, K, w, xf, w_to_bf16=xdt == mx.BF16)
+    err = orc.normwise_rel_err(y.cpu().numpy(), ref)
+    assert err <= TOL, err
+    if xdt == mx.BF16:  # same bf16 weights as the oracle: only accumulation order differs
+        assert err <= 1e-5, err
+    y2 = mx.q_gemm_dequant(x, pw, M, N, K, Q4K, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    assert torch.equal(y, y2)
+
+
 @pytest.mark.parametrize("qt,M,N,K,ydt", [(Q4K, 512, 1024, 4096, "bf16"), (Q6K, 256, 1000, 2048, "f32"),
                                           (Q41, 300, 512, 4096, "bf16"), (Q4K, 40, 1024, 4096, "bf16"),
                                           (Q6K, 64, 512, 2048, "f32"), (Q5K, 17, 768, 1024, "f16"),
@@ -248,8 +267,8 @@ def test_mfma_chunked_launches(cuda, monkeypatch):
 def test_mfma_split_k(cuda, qt, M, N, K, ydt):
     """Split-K through the C ABI: mlxr_qgemm_run_ws with the workspace size the library
     asks for splits K over workgroups (partials + reduce kernel: the skinny kernel for
-    M <= 16 with fewer 32-row slabs than CUs, the tiled kernel otherwise, with 64-row tiles
-    for 16 < M <= 64) and stays within tolerance of the oracle,
+    M <= 32 with few 32-row slabs, the tiled kernel otherwise, with 64-row tiles
+    for 32 < M <= 64) and stays within tolerance of the oracle,
     with bias, for every output dtype and N % 4 != 0; repeated calls are bit-identical, and
     a workspace one byte too small gives exactly the unsplit mlxr_qgemm_run_ex result."""
     import ctypes
