@@ -16,8 +16,8 @@ The other BASELINE configurations are reported under "configs":
 (c1, c3 and c4 time each call inside a replayed hipGraph of back-to-back calls, so host
 launch overhead is not in their figures.)
   c4  Q4_K prefill GEMM, Llama-3-8B set, M in {512, 2048} (bf16 MFMA)
-  c5  Llama-3-70B layer, Q4_K + Q6_K (v, down), 7 GEMMs in a hipGraph at M=1 (grouped as a
-      decoder layer issues them: 5 launches) and M=256 (7 launches)
+  c5  Llama-3-70B layer, Q4_K + Q6_K (v, down), 7 GEMMs in a hipGraph at M=1 and M=256,
+      grouped as a decoder layer issues them (5 launches, plus split-K reduces at M=256)
   mlp (extra) Llama-3-8B gate/up + SwiGLU gating at M=1, fused vs grouped + gating kernel
 The CPU baseline is the reference's CPU path (dequantize all of W to fp32, then the naive
 fp32 loop; restated in oracle/orc.c) on the headline workload, one thread.
@@ -361,8 +361,25 @@ def run_c4(cx, args):
             shapes[n] = {"us": round(us, 1), "TFLOPs": round(f / us / 1e6, 1)}
             tot_f += f
             tot_us += us
+        # the same seven GEMMs as a decoder layer issues them: q/k/v and gate/up as grouped
+        # calls (one tiled launch each), o and down alone -- 4 calls
+        ys = {n: torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev) for n, N, K in LLAMA3_8B}
+        dims = {n: (N, K) for n, N, K in LLAMA3_8B}
+
+        def layer(r):
+            for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+                K = dims[names[0]][1]
+                if len(names) == 1:
+                    n = names[0]
+                    mx.q_gemm_dequant(x[K], W[n], M, dims[n][0], K, Q4K, out=ys[n])
+                else:
+                    mx.q_gemm_dequant_grouped(x[K], [W[n] for n in names], outs=[ys[n] for n in names])
+        layer(0)
+        lus = 1e3 * cx.graph_ms(layer, 2 if M == 2048 else 4)
         res[f"M={M}"] = {"TFLOPs": round(tot_f / tot_us / 1e6, 1),
-                         "frac_bf16_peak": round(tot_f / tot_us / 1e6 / BF16_PEAK_TFLOPS, 4), "shapes": shapes}
+                         "frac_bf16_peak": round(tot_f / tot_us / 1e6 / BF16_PEAK_TFLOPS, 4), "shapes": shapes,
+                         "layer_grouped_4_calls": {"us": round(lus, 1), "TFLOPs": round(tot_f / lus / 1e6, 1),
+                                                   "frac_bf16_peak": round(tot_f / lus / 1e6 / BF16_PEAK_TFLOPS, 4)}}
     # context only: a plain (unquantized) bf16 GEMM of the same gate shape through torch's
     # library path (hipBLASLt), i.e. what the MFMA units give without any dequant work
     M, N, K = 2048, 14336, 4096
@@ -411,15 +428,12 @@ def run_c5(cx, args):
         ys = {n: torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev) for n, N, K, qt in LLAMA3_70B}
 
         def layer_fn(W):
-            if M <= 4:
-                # projections of one input as grouped calls, as a decoder layer issues them:
-                # q,k (Q4_K) in one launch + v (Q6_K), o, gate/up in one launch, down
-                for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
-                    K = dict((n, k) for n, _, k, _ in LLAMA3_70B)[names[0]]
-                    mx.q_gemm_dequant_grouped(x[K], [W[n] for n in names], outs=[ys[n] for n in names])
-                return
-            for n, N, K, qt in LLAMA3_70B:
-                mx.q_gemm_dequant(x[K], W[n], M, N, K, qt, out=ys[n])  # MFMA path at M=256
+            # projections of one input as grouped calls, as a decoder layer issues them:
+            # q,k (Q4_K) in one launch + v (Q6_K), o, gate/up in one launch, down (GEMV at
+            # M = 1, tiled MFMA GEMM at M = 256)
+            for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+                K = dict((n, k) for n, _, k, _ in LLAMA3_70B)[names[0]]
+                mx.q_gemm_dequant_grouped(x[K], [W[n] for n in names], outs=[ys[n] for n in names])
         graphs = [cx.graph(lambda W=W: layer_fn(W)) for W in copies]
         for r in range(2):
             graphs[r % len(graphs)].replay()
@@ -427,12 +441,24 @@ def run_c5(cx, args):
         ms = cx.event_ms(lambda r: graphs[r % len(graphs)].replay(), 10 if M == 1 else 4)
         byts = sum(gemm_bytes(mx, qt, M, N, K) for _, N, K, qt in LLAMA3_70B)
         flops = sum(2.0 * M * N * K for _, N, K, qt in LLAMA3_70B)
-        res[f"M={M}"] = {"ms_per_layer": round(ms, 4), "launches_per_layer": 5 if M <= 4 else 7,
+        res[f"M={M}"] = {"ms_per_layer": round(ms, 4), "launches_per_layer": 5,
                          "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
                          "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
                          "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
         del graphs
+        if M > 4:
+            # beside it: the seven projections as seven separate calls
+            def sep_fn(W):
+                for n, N, K, qt in LLAMA3_70B:
+                    mx.q_gemm_dequant(x[K], W[n], M, N, K, qt, out=ys[n])
+            graphs = [cx.graph(lambda W=W: sep_fn(W)) for W in copies]
+            graphs[0].replay()
+            torch.cuda.synchronize()
+            ms7 = cx.event_ms(lambda r: graphs[r % len(graphs)].replay(), 4)
+            res[f"M={M}"]["separate_7_calls"] = {"ms_per_layer": round(ms7, 4),
+                                                 "TFLOPs": round(flops / (ms7 * 1e-3) / 1e12, 1)}
+            del graphs
     return res
 
 

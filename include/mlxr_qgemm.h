@@ -153,13 +153,26 @@ typedef struct mlxr_qgemm_item {
 
 /* y_i[M, N_i] = X[M, K] . W_i[N_i, K]^T (+ bias_i) for `count` weights that read the same
  * activations -- the projections of one input, e.g. q/k/v or gate/up of a decoder layer.
- * Every item must have the same K.  Items of one quant type at M <= 4 run in a single
- * launch (up to four per launch) that stages X once; other items run as
+ * Every item must have the same K.  Items of one quant type run up to four per launch
+ * where the kernel allows it: the GEMV at M <= 4 (X staged once) and the tiled MFMA GEMM
+ * at M > 64 (tile columns of the weights side by side); other items run as
  * mlxr_qgemm_run(..., MLXR_PATH_AUTO).  Results equal count separate mlxr_qgemm_run calls
  * bit for bit.  No counterpart in the reference (its Linear layers call q_gemm_dequant one
- * projection at a time, core/graph/layers.cpp:86-99); it exists to cut kernel launches. */
+ * projection at a time, core/graph/layers.cpp:86-99); it exists to cut kernel launches
+ * and, for prefill, to fill the device with the small projections' tiles. */
 int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
                            void* stream);
+/* mlxr_qgemm_run_grouped with a caller-owned device workspace (NULL or too small = as
+ * mlxr_qgemm_run_grouped).  With it the tiled launches also serve 32 < M <= 64 and split K
+ * over the concatenated N of their weights when their tiles cannot fill the device, and
+ * single items run as mlxr_qgemm_run_ws.  Results then differ from separate calls only in
+ * fp32 summation order (within the matmul tolerance) and are deterministic for a given
+ * (items, M, workspace size).  Same workspace rules as mlxr_qgemm_run_ws. */
+int mlxr_qgemm_run_grouped_ws(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
+                              void* workspace_dev, size_t workspace_bytes, void* stream);
+/* Workspace bytes mlxr_qgemm_run_grouped_ws can use for these items at this M (only the
+ * items' qtype, N and K are read). */
+int mlxr_qgemm_grouped_workspace_size(int count, const mlxr_qgemm_item* items, int M, size_t* bytes);
 
 /* h[M, N] = swish(X . Wg^T) * (X . Wu^T): the gate/up half of a SwiGLU MLP
  * (reference core/graph/layers.cpp:391-414; swiglu_mlp_fused.metal:131-345 plans the

@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
@@ -231,21 +232,60 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   return MLXR_OK;
 }
 
-int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
-                           void* stream) {
+namespace {
+
+// How a grouped call runs its items: launches of several items (GEMV at M <= 4, tiled MFMA
+// where the tiled kernel serves the call) and single calls for the rest.
+struct Batch {
+  int kind;  // 0 single call, 1 grouped GEMV, 2 grouped tiled MFMA
+  int idx[4];
+  int n;
+};
+std::vector<Batch> plan_batches(const std::vector<mlxr::RunArgs>& a, int M, bool with_ws) {
+  const int count = (int)a.size();
+  const bool tiled = M > 64 || (M > skinny_only_max_m() && with_ws);
+  std::vector<bool> done((size_t)count, false);
+  std::vector<Batch> out;
+  for (int i = 0; i < count; ++i) {
+    if (done[i]) continue;
+    const int kind = (M <= kGemvMaxM && mlxr::gemv_groupable(a[i])) ? 1 : (tiled && mlxr::mfma_groupable(a[i])) ? 2 : 0;
+    Batch bt{kind, {i, 0, 0, 0}, 1};
+    done[i] = true;
+    if (kind != 0) {
+      for (int j = i + 1; j < count && bt.n < 4; ++j) {
+        if (done[j] || a[j].L.qtype != a[i].L.qtype) continue;
+        if (kind == 1 ? !mlxr::gemv_groupable(a[j]) : !mlxr::mfma_groupable(a[j])) continue;
+        bt.idx[bt.n++] = j;
+        done[j] = true;
+      }
+    }
+    out.push_back(bt);
+  }
+  return out;
+}
+
+// Validates the items (each exactly as a single call) and fills their run arguments.
+int grouped_args(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M, bool need_ptrs,
+                 void* stream, std::vector<mlxr::RunArgs>& a) {
   if (count < 0 || (count > 0 && !items)) return fail(MLXR_E_INVALID, "invalid item list");
+  a.resize((size_t)count);
   if (count == 0) return MLXR_OK;
-  std::vector<mlxr::RunArgs> a((size_t)count);
   const int K = items[0].K;
+  if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
   for (int i = 0; i < count; ++i) {
     const mlxr_qgemm_item& it = items[i];
     if (it.K != K) return fail(MLXR_E_SHAPE, "grouped items must share K (item %d has K=%d, item 0 K=%d)", i, it.K, K);
-    // full validation of each item, exactly as a single call would do it
-    int rc = mlxr_qgemm_run_ex(it.qtype, it.N, it.K, it.group_size, it.packed_dev, x_dev, x_dtype, it.bias_dev,
-                               it.bias_dtype, it.y_dev, it.y_dtype, 0, MLXR_PATH_AUTO, stream);
-    if (rc) return rc;
-    if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
-    if (M > 0 && (!it.packed_dev || !x_dev || !it.y_dev)) return fail(MLXR_E_INVALID, "null buffer (item %d)", i);
+    if (need_ptrs) {
+      // full validation of each item, exactly as a single call would do it
+      int rc = mlxr_qgemm_run_ex(it.qtype, it.N, it.K, it.group_size, it.packed_dev, x_dev, x_dtype, it.bias_dev,
+                                 it.bias_dtype, it.y_dev, it.y_dtype, 0, MLXR_PATH_AUTO, stream);
+      if (rc) return rc;
+      if (M > 0 && (!it.packed_dev || !x_dev || !it.y_dev)) return fail(MLXR_E_INVALID, "null buffer (item %d)", i);
+    } else {
+      mlxr::PackedLayout L;
+      int rc = check_type_shape(it.qtype, it.N, it.K, &L);
+      if (rc) return rc;
+    }
     mlxr::make_layout(it.qtype, it.N, it.K, &a[i].L);
     a[i].packed = (const uint8_t*)it.packed_dev;
     a[i].x = x_dev;
@@ -256,30 +296,68 @@ int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* 
     a[i].y_dtype = it.y_dtype;
     a[i].M = M;
   }
-  if (M == 0) return MLXR_OK;
+  return MLXR_OK;
+}
+
+int run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M, void* ws,
+                size_t ws_bytes, void* stream) {
+  std::vector<mlxr::RunArgs> a;
+  int rc = grouped_args(count, items, x_dev, x_dtype, M, true, stream, a);
+  if (rc || count == 0 || M == 0) return rc;
   hipStream_t s = (hipStream_t)stream;
-  std::vector<bool> done((size_t)count, false);
-  for (int i = 0; i < count; ++i) {
-    if (done[i]) continue;
-    if (!mlxr::gemv_groupable(a[i])) {
-      const mlxr_qgemm_item& it = items[i];
-      int rc = mlxr_qgemm_run_ex(it.qtype, it.N, it.K, it.group_size, it.packed_dev, x_dev, x_dtype, it.bias_dev,
-                                 it.bias_dtype, it.y_dev, it.y_dtype, M, MLXR_PATH_AUTO, stream);
-      if (rc) return rc;
-      done[i] = true;
-      continue;
-    }
-    // gather up to four groupable items of this quant type into one launch
+  for (const Batch& bt : plan_batches(a, M, ws != nullptr)) {
     const mlxr::RunArgs* batch[4];
-    int nb = 0;
-    for (int j = i; j < count && nb < 4; ++j)
-      if (!done[j] && a[j].L.qtype == a[i].L.qtype && mlxr::gemv_groupable(a[j])) {
-        batch[nb++] = &a[j];
-        done[j] = true;
-      }
-    const hipError_t e = mlxr::launch_gemv_grouped(batch, nb, s);
-    if (e != hipSuccess) return hip_fail(e, "grouped gemv launch");
+    for (int k = 0; k < bt.n; ++k) batch[k] = &a[(size_t)bt.idx[k]];
+    if (bt.kind == 1) {
+      const hipError_t e = mlxr::launch_gemv_grouped(batch, bt.n, s);
+      if (e != hipSuccess) return hip_fail(e, "grouped gemv launch");
+    } else if (bt.kind == 2) {
+      const hipError_t e = mlxr::launch_mfma_grouped(batch, bt.n, ws, ws ? ws_bytes : 0, s);
+      if (e != hipSuccess) return hip_fail(e, "grouped mfma launch");
+    } else {
+      const mlxr_qgemm_item& it = items[bt.idx[0]];
+      rc = mlxr_qgemm_run_ws(it.qtype, it.N, it.K, it.group_size, it.packed_dev, x_dev, x_dtype, it.bias_dev,
+                             it.bias_dtype, it.y_dev, it.y_dtype, M, MLXR_PATH_AUTO, ws, ws ? ws_bytes : 0, stream);
+      if (rc) return rc;
+    }
   }
+  return MLXR_OK;
+}
+
+}  // namespace
+
+int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
+                           void* stream) {
+  return run_grouped(count, items, x_dev, x_dtype, M, nullptr, 0, stream);
+}
+
+int mlxr_qgemm_run_grouped_ws(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
+                              void* workspace_dev, size_t workspace_bytes, void* stream) {
+  return run_grouped(count, items, x_dev, x_dtype, M, workspace_dev, workspace_dev ? workspace_bytes : 0, stream);
+}
+
+int mlxr_qgemm_grouped_workspace_size(int count, const mlxr_qgemm_item* items, int M, size_t* bytes) {
+  if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
+  std::vector<mlxr::RunArgs> a;
+  int rc = grouped_args(count, items, nullptr, MLXR_BF16, M, false, nullptr, a);
+  if (rc) return rc;
+  size_t need = 0;
+  if (count > 0 && M > 0) {
+    for (const Batch& bt : plan_batches(a, M, true)) {
+      const mlxr::RunArgs* batch[4];
+      for (int k = 0; k < bt.n; ++k) batch[k] = &a[(size_t)bt.idx[k]];
+      size_t b = 0;
+      if (bt.kind == 2) {
+        b = mlxr::mfma_grouped_workspace_bytes(batch, bt.n);
+      } else if (bt.kind == 0) {
+        const mlxr_qgemm_item& it = items[bt.idx[0]];
+        rc = mlxr_qgemm_workspace_size(it.qtype, it.N, it.K, M, &b);
+        if (rc) return rc;
+      }
+      need = std::max(need, b);
+    }
+  }
+  *bytes = need;
   return MLXR_OK;
 }
 

@@ -55,6 +55,12 @@ hipError_t launch_gemv_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_
 hipError_t launch_mfma(const RunArgs& a, hipStream_t s);
 // Workspace bytes launch_mfma would use for an [M, N, K] problem (0: no split).
 size_t mfma_workspace_bytes(int M, int N, int K);
+// Up to 4 weights of one quant type and K sharing x and M in one tiled launch (their tile
+// columns side by side; split-K over the concatenated N when ws holds the partials).
+// mfma_groupable() tells whether an item qualifies (every operand below 2 GiB).
+bool mfma_groupable(const RunArgs& a);
+hipError_t launch_mfma_grouped(const RunArgs* const* items, int n, void* ws, size_t ws_bytes, hipStream_t s);
+size_t mfma_grouped_workspace_bytes(const RunArgs* const* items, int n);
 
 // Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.  With a.ws,
 // shapes with fewer 32-row slabs than CUs also split K over workgroups.

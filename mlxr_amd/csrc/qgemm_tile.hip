@@ -36,6 +36,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -59,20 +60,31 @@ constexpr int NSTAGE = 4;              // activation stages (DMA three steps ahe
 template <int QT>
 constexpr int prefetch_steps() { return QT == QT_Q8_0 ? 4 : 8; }
 
-struct TileParams {
-  const void* x;
-  const void* bias;
-  void* y;
+// One weight of a launch.  A launch covers up to MAX_TG weights that share X, K and the
+// quant type (grouped projections): their tile columns follow each other.
+constexpr int MAX_TG = 4;
+struct TileGroup {
   const uint8_t* P[4];
   uint32_t psize[4];
-  int M, N, K;
-  int ldy;  // row stride of y in elements
+  void* y;
+  const void* bias;
+  int N;
+  int ldy;   // row stride of y in elements
+  int tn0;   // first tile column of this weight in the launch
+  int col0;  // first column of this weight in a split-K workspace row
   int bias_dtype, y_dtype;
-  int tiles_m, tiles_n;
+};
+struct TileParams {
+  const void* x;
+  int M, K;
+  int tiles_m, tiles_n;  // tiles_n: over all weights of the launch
   int kps;          // K steps per split (multiple of 4); the grid is tiles x splits
-  float* ws;        // split-K: fp32 partials, split s at ws + s * ws_split (row stride ldy)
+  float* ws;        // split-K: fp32 partials, split s at ws + s * ws_split, rows of ws_ld
   size_t ws_split;  // elements per split plane
-  uint32_t nib;  // 0x0F0F0F0F, passed at run time (keeps the byte converts)
+  int ws_ld;        // workspace row stride (the launch's total N)
+  uint32_t nib;     // 0x0F0F0F0F, passed at run time (keeps the byte converts)
+  int ngroups;
+  TileGroup g[MAX_TG];
 };
 
 // LDS position of 16-byte chunk c of activation row r in a stage: c ^ swz(r).  Fragment
@@ -124,8 +136,33 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   int t = b;
   if ((ntiles & 7) == 0) t = (b & 7) * (ntiles >> 3) + (b >> 3);
   const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
-  const int m0 = tm * BM, n0 = tn * TN;
-  const int M = p.M, N = p.N, K = p.K;
+  // the weight this tile column belongs to (scalar search), its fields selected with
+  // static kernel-argument offsets so every load is issued at once
+  int gi = 0;
+#pragma unroll
+  for (int g = 1; g < MAX_TG; ++g)
+    if (g < p.ngroups && tn >= p.g[g].tn0) gi = g;
+  TileGroup G = p.g[0];
+#pragma unroll
+  for (int g = 1; g < MAX_TG; ++g) {
+    const TileGroup& H = p.g[g];
+    const bool sel = g == gi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      G.P[i] = sel ? H.P[i] : G.P[i];
+      G.psize[i] = sel ? H.psize[i] : G.psize[i];
+    }
+    G.y = sel ? H.y : G.y;
+    G.bias = sel ? H.bias : G.bias;
+    G.N = sel ? H.N : G.N;
+    G.ldy = sel ? H.ldy : G.ldy;
+    G.tn0 = sel ? H.tn0 : G.tn0;
+    G.col0 = sel ? H.col0 : G.col0;
+    G.bias_dtype = sel ? H.bias_dtype : G.bias_dtype;
+    G.y_dtype = sel ? H.y_dtype : G.y_dtype;
+  }
+  const int m0 = tm * BM, n0 = (tn - G.tn0) * TN;
+  const int M = p.M, N = G.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK - 1) / TK;
   // this workgroup's K steps [kt0, kend): kt0 is a multiple of four (super-block start)
@@ -133,7 +170,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
 
   rsrc_t R[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P[i] ? p.P[i] : (const uint8_t*)p.x, p.psize[i]);
+  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(G.P[i] ? G.P[i] : (const uint8_t*)p.x, G.psize[i]);
 
   // --- activations: LDS DMA.  Wave w fills slot blocks MI*w .. MI*w+MI-1 of a stage
   // (1 KiB = 8 rows each); lane l of block b brings row 8b + l/8, global chunk
@@ -338,14 +375,17 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   float* ep = (float*)lds + wave * (32 * EP_LD);
   const int c4 = lane & 15;
   const int ncol = n0 + 64 * wave + 4 * c4;  // first of this lane's four columns
-  const bool vec_ok = (N & 3) == 0 && (p.ldy & 3) == 0 && ncol + 3 < N;
+  // output rows: y's, or the workspace's (split plane, this weight's column range)
+  const int ld = p.ws ? p.ws_ld : G.ldy;
+  const int cb = p.ws ? G.col0 : 0;
+  const bool vec_ok = (N & 3) == 0 && ((ld | cb) & 3) == 0 && ncol + 3 < N;
   float bv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (!p.ws && p.bias) {
+  if (!p.ws && G.bias) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) bv[e] = ncol + e < N ? load_scalar(p.bias, p.bias_dtype, ncol + e) : 0.f;
+    for (int e = 0; e < 4; ++e) bv[e] = ncol + e < N ? load_scalar(G.bias, G.bias_dtype, ncol + e) : 0.f;
   }
-  void* const out = p.ws ? (void*)(p.ws + (size_t)split * p.ws_split) : p.y;
-  const int yt = p.ws ? DT_F32 : p.y_dtype;
+  void* const out = p.ws ? (void*)(p.ws + (size_t)split * p.ws_split) : G.y;
+  const int yt = p.ws ? DT_F32 : G.y_dtype;
   sfor<MI>([&](auto I_) {
     constexpr int i = decltype(I_)::value;
 #pragma unroll
@@ -362,7 +402,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
       const int m = m0 + 32 * i + row;
       if (m < M) {
         const float o[4] = {v.x + bv[0], v.y + bv[1], v.z + bv[2], v.w + bv[3]};
-        const size_t at = (size_t)m * (size_t)p.ldy + (size_t)ncol;
+        const size_t at = (size_t)m * (size_t)ld + (size_t)(cb + ncol);
         if (vec_ok) {
           if (yt == DT_F32) *(float4*)((float*)out + at) = make_float4(o[0], o[1], o[2], o[3]);
           else if (yt == DT_BF16)
@@ -383,12 +423,16 @@ template <int QT, int XT, int MI>
 hipError_t launch_tile_t(const TileParams& tp, int nblocks, hipStream_t s) {
   // activation stages, or the epilogue's four 32 x 68 fp32 blocks if larger (MI = 2)
   constexpr int lds_bytes = std::max(NSTAGE * 32 * MI * TK * 2, 4 * 32 * 68 * 4);
-  static bool attr_set = false;
-  if (!attr_set) {
+  // the LDS limit is a per-device attribute of the kernel: set once on each device used
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(attr_set.load(std::memory_order_acquire) & bit)) {
     const hipError_t e = hipFuncSetAttribute((const void*)qgemm_tile_kernel<QT, XT, MI>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set.fetch_or(bit, std::memory_order_release);
   }
   qgemm_tile_kernel<QT, XT, MI><<<dim3((unsigned)nblocks), dim3(256), lds_bytes, s>>>(tp);
   return hipGetLastError();
@@ -446,10 +490,10 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
   return best;
 }
 
+// tp.tiles_n and the groups' tn0 are set by the caller
 template <int QT, int XT>
 hipError_t launch_q(TileParams tp, int bm, int S, hipStream_t s) {
   tp.tiles_m = (tp.M + bm - 1) / bm;
-  tp.tiles_n = (tp.N + TN - 1) / TN;
   const int ntiles = tp.tiles_m * tp.tiles_n;
   if (bm == 64) return launch_tile_t<QT, XT, 2>(tp, ntiles * S, s);
   return bm == 128 ? launch_tile_t<QT, XT, 4>(tp, ntiles * S, s) : launch_tile_t<QT, XT, 8>(tp, ntiles * S, s);
@@ -491,6 +535,30 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   } else {
     store_scalar(y, y_dtype, i, v[0]);
   }
+}
+
+// Grouped split-K: the partial planes hold the launch's weights side by side (rows of
+// ws_ld = total N); element (m, c) goes to the weight whose column range holds c.
+struct ReduceGroups {
+  void* y[MAX_TG];
+  const void* bias[MAX_TG];
+  int col0[MAX_TG], N[MAX_TG], y_dtype[MAX_TG], bias_dtype[MAX_TG];
+  int ngroups;
+};
+__global__ __launch_bounds__(256) void splitk_reduce_grouped_kernel(const float* __restrict__ ws, size_t split_elems,
+                                                                    int S, int ws_ld, size_t total, ReduceGroups rg) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  float v = ws[i];
+  for (int sp = 1; sp < S; ++sp) v += ws[(size_t)sp * split_elems + i];
+  const int m = (int)(i / (size_t)ws_ld), c = (int)(i - (size_t)m * ws_ld);
+  int g = 0;
+#pragma unroll
+  for (int k = 1; k < MAX_TG; ++k)
+    if (k < rg.ngroups && c >= rg.col0[k]) g = k;
+  const int n = c - rg.col0[g];
+  if (rg.bias[g]) v += load_scalar(rg.bias[g], rg.bias_dtype[g], n);
+  store_scalar(rg.y[g], rg.y_dtype[g], (size_t)m * rg.N[g] + n, v);
 }
 
 hipError_t launch_chunk(const TileParams& tp, int bm, int S, int qtype, bool f16, hipStream_t s) {
@@ -537,22 +605,28 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   if (sp.S > 1) {
     TileParams tp;
     tp.M = M;
-    tp.N = N;
     tp.K = K;
-    tp.ldy = N;
-    for (int i = 0; i < 4; ++i) {
-      tp.P[i] = P.p[i];
-      tp.psize[i] = i < a.L.nplanes ? (uint32_t)a.L.size[i] : 0u;
-    }
     tp.x = a.x;
-    tp.y = a.y;
-    tp.bias = nullptr;
-    tp.bias_dtype = a.bias_dtype;
-    tp.y_dtype = DT_F32;
     tp.nib = 0x0F0F0F0Fu;
     tp.kps = sp.kps;
     tp.ws = (float*)a.ws;
     tp.ws_split = (size_t)M * (size_t)N;
+    tp.ws_ld = N;
+    tp.ngroups = 1;
+    TileGroup& g = tp.g[0];
+    for (int i = 0; i < 4; ++i) {
+      g.P[i] = P.p[i];
+      g.psize[i] = i < a.L.nplanes ? (uint32_t)a.L.size[i] : 0u;
+    }
+    g.y = a.y;
+    g.bias = nullptr;
+    g.N = N;
+    g.ldy = N;
+    g.tn0 = 0;
+    g.col0 = 0;
+    g.bias_dtype = a.bias_dtype;
+    g.y_dtype = DT_F32;
+    tp.tiles_n = (N + TN - 1) / TN;
     hipError_t e = launch_chunk(tp, sp.bm, sp.S, a.L.qtype, a.x_dtype == DT_F16, s);
     if (e != hipSuccess) return e;
     return launch_splitk_reduce((const float*)a.ws, tp.ws_split, sp.S, a.bias, a.bias_dtype, a.y, a.y_dtype, M, N,
@@ -562,28 +636,121 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
     for (int nc = 0; nc < N; nc += Nc) {
       TileParams tp;
       tp.M = std::min(Mc, M - mc);
-      tp.N = std::min(Nc, N - nc);
       tp.K = K;
-      tp.ldy = N;
-      for (int i = 0; i < 4; ++i) {
-        tp.P[i] = P.p[i] ? P.p[i] + (size_t)nc * prb[i] : nullptr;
-        tp.psize[i] = i < a.L.nplanes ? (uint32_t)((size_t)tp.N * prb[i]) : 0u;
-      }
       tp.x = (const uint8_t*)a.x + (size_t)mc * K * 2;
-      tp.y = (uint8_t*)a.y + ((size_t)mc * N + nc) * ye;
-      tp.bias = a.bias ? (const uint8_t*)a.bias + (size_t)nc * be : nullptr;
-      tp.bias_dtype = a.bias_dtype;
-      tp.y_dtype = a.y_dtype;
       tp.nib = 0x0F0F0F0Fu;
       tp.kps = (K + TK - 1) / TK;
       tp.ws = nullptr;
       tp.ws_split = 0;
-      const int bm = plan_split(tp.M, tp.N, K, 0).bm;
+      tp.ws_ld = 0;
+      tp.ngroups = 1;
+      TileGroup& g = tp.g[0];
+      g.N = std::min(Nc, N - nc);
+      for (int i = 0; i < 4; ++i) {
+        g.P[i] = P.p[i] ? P.p[i] + (size_t)nc * prb[i] : nullptr;
+        g.psize[i] = i < a.L.nplanes ? (uint32_t)((size_t)g.N * prb[i]) : 0u;
+      }
+      g.y = (uint8_t*)a.y + ((size_t)mc * N + nc) * ye;
+      g.bias = a.bias ? (const uint8_t*)a.bias + (size_t)nc * be : nullptr;
+      g.ldy = N;
+      g.tn0 = 0;
+      g.col0 = 0;
+      g.bias_dtype = a.bias_dtype;
+      g.y_dtype = a.y_dtype;
+      tp.tiles_n = (g.N + TN - 1) / TN;
+      const int bm = plan_split(tp.M, g.N, K, 0).bm;
       const hipError_t e = launch_chunk(tp, bm, 1, a.L.qtype, a.x_dtype == DT_F16, s);
       if (e != hipSuccess) return e;
     }
   }
   return hipSuccess;
+}
+
+// Grouped launch: up to MAX_TG weights of one quant type and K that share x, as one grid
+// whose tile columns run over the weights in turn; the split plan is that of the
+// concatenated N.  Requires every operand below 2 GiB (mfma_groupable).
+bool mfma_groupable(const RunArgs& a) {
+  if ((size_t)a.M * (size_t)a.L.K * 2u >= ((size_t)1 << 31)) return false;
+  for (int i = 0; i < a.L.nplanes; ++i)
+    if (a.L.size[i] >= ((size_t)1 << 31)) return false;
+  return true;
+}
+
+static int grouped_cols(const RunArgs* const* items, int n, int* ntiles) {
+  int cols = 0, t = 0;
+  for (int i = 0; i < n; ++i) {
+    cols += items[i]->L.N;
+    t += (items[i]->L.N + TN - 1) / TN;
+  }
+  if (ntiles) *ntiles = t;
+  return cols;
+}
+
+size_t mfma_grouped_workspace_bytes(const RunArgs* const* items, int n) {
+  int nt = 0;
+  const int cols = grouped_cols(items, n, &nt);
+  const RunArgs& a = *items[0];
+  if (!mfma_groupable(a)) return 0;
+  const SplitPlan sp = plan_split(a.M, nt * TN, a.L.K, ~(size_t)0);
+  return sp.S > 1 ? (size_t)sp.S * (size_t)a.M * (size_t)cols * 4u : 0;
+}
+
+hipError_t launch_mfma_grouped(const RunArgs* const* items, int n, void* ws, size_t ws_bytes, hipStream_t s) {
+  const RunArgs& a = *items[0];
+  const int M = a.M, K = a.L.K;
+  int nt = 0;
+  const int cols = grouped_cols(items, n, &nt);
+  SplitPlan sp = plan_split(M, nt * TN, K, ~(size_t)0);
+  if (sp.S > 1 && (!ws || (size_t)sp.S * (size_t)M * (size_t)cols * 4u > ws_bytes)) sp = plan_split(M, nt * TN, K, 0);
+  TileParams tp;
+  tp.M = M;
+  tp.K = K;
+  tp.x = a.x;
+  tp.nib = 0x0F0F0F0Fu;
+  tp.kps = sp.S > 1 ? sp.kps : (K + TK - 1) / TK;
+  tp.ws = sp.S > 1 ? (float*)ws : nullptr;
+  tp.ws_split = (size_t)M * (size_t)cols;
+  tp.ws_ld = cols;
+  tp.ngroups = n;
+  tp.tiles_n = nt;
+  ReduceGroups rg;
+  rg.ngroups = n;
+  int tn0 = 0, col0 = 0;
+  for (int i = 0; i < MAX_TG; ++i) {
+    TileGroup& g = tp.g[i];
+    if (i >= n) {  // unused entries: never selected (ngroups), kept defined
+      g = tp.g[0];
+      continue;
+    }
+    const RunArgs& b = *items[i];
+    const PlanePtrs P = plane_ptrs(b.L, b.packed);
+    for (int k = 0; k < 4; ++k) {
+      g.P[k] = P.p[k];
+      g.psize[k] = k < b.L.nplanes ? (uint32_t)b.L.size[k] : 0u;
+    }
+    g.y = b.y;
+    g.bias = sp.S > 1 ? nullptr : b.bias;
+    g.N = b.L.N;
+    g.ldy = b.L.N;
+    g.tn0 = tn0;
+    g.col0 = col0;
+    g.bias_dtype = b.bias_dtype;
+    g.y_dtype = b.y_dtype;
+    rg.y[i] = b.y;
+    rg.bias[i] = b.bias;
+    rg.col0[i] = col0;
+    rg.N[i] = b.L.N;
+    rg.y_dtype[i] = b.y_dtype;
+    rg.bias_dtype[i] = b.bias_dtype;
+    tn0 += (b.L.N + TN - 1) / TN;
+    col0 += b.L.N;
+  }
+  hipError_t e = launch_chunk(tp, sp.bm, sp.S > 1 ? sp.S : 1, a.L.qtype, a.x_dtype == DT_F16, s);
+  if (e != hipSuccess || sp.S <= 1) return e;
+  const size_t total = (size_t)M * (size_t)cols;
+  splitk_reduce_grouped_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
+      (const float*)ws, tp.ws_split, sp.S, cols, total, rg);
+  return hipGetLastError();
 }
 
 size_t mfma_workspace_bytes(int M, int N, int K) {

@@ -74,6 +74,8 @@ _SIGS = {
     "mlxr_qgemm_swiglu": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "mlxr_swiglu": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run_grouped": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "mlxr_qgemm_run_grouped_ws": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mlxr_qgemm_grouped_workspace_size": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
 }
@@ -256,10 +258,12 @@ def workspace_size(qtype, N, K, M):
     return out.value
 
 
-def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=None, stream=None):
+def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=None, stream=None, workspace=True):
     """y_i = input . W_i^T (+ bias_i) for packed weights that read the same input (e.g. the
     q/k/v or gate/up projections), in as few launches as the library can (one per four
-    same-type weights at M <= 4).  Returns the list of outputs."""
+    same-type weights at M <= 4 and in the tiled GEMM).  With `workspace` (default) the
+    library's split-K workspace comes from torch's allocator (mlxr_qgemm_run_grouped_ws);
+    without it the call is mlxr_qgemm_run_grouped.  Returns the list of outputs."""
     torch = _torch()
     M, K = input.shape
     if not input.is_contiguous():
@@ -274,7 +278,17 @@ def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=Non
             raise QGemmError(-3, "Input shape must be [M, K]")
         arr[i] = Item(int(w.qtype), w.N, w.K, 0, w.data_ptr(), b.data_ptr() if b is not None else None,
                       _dt_code(b.dtype) if b is not None else F32, y.data_ptr(), _dt_code(y.dtype))
-    _check(lib().mlxr_qgemm_run_grouped(n, arr, input.data_ptr(), _dt_code(input.dtype), M, _stream_ptr(stream)))
+    if not workspace:
+        _check(lib().mlxr_qgemm_run_grouped(n, arr, input.data_ptr(), _dt_code(input.dtype), M, _stream_ptr(stream)))
+        return outs
+    nb = ctypes.c_size_t(0)
+    _check(lib().mlxr_qgemm_grouped_workspace_size(n, arr, M, ctypes.byref(nb)))
+    ws = None
+    if nb.value:
+        with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+            ws = torch.empty(nb.value, dtype=torch.uint8, device=input.device)
+    _check(lib().mlxr_qgemm_run_grouped_ws(n, arr, input.data_ptr(), _dt_code(input.dtype), M,
+                                           ws.data_ptr() if ws is not None else None, nb.value, _stream_ptr(stream)))
     return outs
 
 

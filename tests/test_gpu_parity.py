@@ -4,6 +4,8 @@ Bars: packed bytes and fp32 dequant bit-exact; bf16 dequant bit-exact to RNE_bf1
 oracle; matmul outputs within max|y-ref|/max|ref| <= 5e-3 of the fp64-accumulated oracle
 (GEMV over the exact weights, MFMA over the bf16-rounded weights it consumes).
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -205,6 +207,40 @@ def test_grouped_equals_separate_calls(cuda, M):
         ref = orc.gemm_f64(int(w.qtype), M, w.N, K, mx.synth_gguf(w.qtype, w.N, K, 200 + i), xf,
                            bias=None if biases[i] is None else biases[i].float().cpu().numpy())
         assert orc.normwise_rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K", [(65, 1024), (130, 4096), (300, 2048), (48, 4096)])
+def test_grouped_tiled_launches(cuda, M, K):
+    """Grouped calls on the tiled MFMA GEMM: same-type weights share one launch (tile columns
+    side by side).  Without a workspace the launch is unsplit and equals separate calls bit
+    for bit (M > 64); with the workspace the library asks for, the concatenated N may split
+    K (also for 32 < M <= 64) and stays within tolerance of the oracle, deterministically,
+    with a bias, a ragged N and a mixed-type group."""
+    import torch
+    specs = [(Q4K, 512), (Q4K, 130), (Q6K, 128), (Q4K, 640), (Q4K, 256)]
+    gg = [mx.synth_gguf(qt, N, K, 300 + i) for i, (qt, N) in enumerate(specs)]
+    ws = [mx.pack_weights(g, N, K, qt, device=cuda) for g, (qt, N) in zip(gg, specs)]
+    x, xf = _act(torch, M, K, mx.BF16, 310, cuda)
+    bias = torch.linspace(-1, 1, 130, device=cuda).to(torch.bfloat16)
+    biases = [None, bias, None, None, None]
+    if M > 64:
+        ys = mx.q_gemm_dequant_grouped(x, ws, biases=biases, out_dtype=torch.float32, workspace=False)
+        for i, (w, y) in enumerate(zip(ws, ys)):
+            y1 = torch.empty_like(y)
+            L = mx.lib()
+            rc = L.mlxr_qgemm_run_ex(int(w.qtype), w.N, K, 0, w.data_ptr(), x.data_ptr(), mx.BF16,
+                                     biases[i].data_ptr() if biases[i] is not None else None, mx.BF16,
+                                     y1.data_ptr(), mx.F32, M, mx.PATH_AUTO,
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            assert rc == 0, L.mlxr_qgemm_last_error()
+            assert torch.equal(y, y1), i
+    yw = mx.q_gemm_dequant_grouped(x, ws, biases=biases, out_dtype=torch.float32)
+    yw2 = mx.q_gemm_dequant_grouped(x, ws, biases=biases, out_dtype=torch.float32)
+    for i, (w, y, y2) in enumerate(zip(ws, yw, yw2)):
+        assert torch.equal(y, y2), i
+        ref = orc.gemm_f64(int(w.qtype), M, w.N, K, gg[i], xf, w_to_bf16=True,
+                           bias=None if biases[i] is None else biases[i].float().cpu().numpy())
+        assert orc.normwise_rel_err(y.cpu().numpy(), ref) <= TOL, i
 
 
 @pytest.mark.parametrize("qt,M,N,K", [(Q4K, 300, 512, 4096), (Q6K, 256, 256, 2048), (Q80, 130, 384, 1056),
