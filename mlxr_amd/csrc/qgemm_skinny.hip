@@ -1,5 +1,7 @@
 // Skinny GEMM for 4 < M <= 64 (batched decode): Y[M,N] = X[M,K] . W[N,K]^T (+ bias) on
-// 32x32x16 MFMA, streaming every weight byte from HBM exactly once.
+// MFMA, streaming every weight byte from HBM exactly once.  Two variants: the one below
+// on 32x32x16 MFMA (32 < M <= 64), and a narrow one further down on 16x16x32 MFMA for
+// M <= 32 (qgemm_skinny16_kernel).
 //
 // At these M the VALU dot products of the GEMV kernel cost M/2 operations per weight and
 // fall far behind HBM; here each weight is dequantized once in registers (the routines
