@@ -1,4 +1,4 @@
-// Buffer loads and wait helpers shared by the MFMA kernels (qgemm_tile.hip,
+// Buffer loads and wait helpers shared by the MFMA kernels (qgemm_tile_kernel.h,
 // qgemm_skinny.hip).
 #pragma once
 #include <hip/hip_runtime.h>

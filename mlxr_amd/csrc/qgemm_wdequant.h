@@ -1,5 +1,5 @@
 // Register dequantization of packed weights into MFMA operand words, shared by the MFMA
-// GEMM (qgemm_tile.hip) and the dequant entry point (qgemm_pack.hip), so the values the
+// GEMM (qgemm_tile_kernel.h) and the dequant entry point (qgemm_pack.hip), so the values the
 // GEMM multiplies are exactly the ones mlxr_qgemm_dequant returns.
 //
 // A "word" is 8 consecutive weights of a 32-weight sub-block (word kk = weights 8kk ..
