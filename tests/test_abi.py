@@ -129,3 +129,38 @@ def test_cpp_operator_interface(tmp_path):
     subprocess.run(cmd, check=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.startswith("OK"), r.stdout + r.stderr
+
+
+def test_workspace_queries():
+    """Workspace sizes need no device: zero where nothing splits (GEMV sizes, M = 0), whole
+    planes of M x N fp32 partials otherwise, and for a grouped call the largest need of its
+    launches (same-type items share one launch in the tiled GEMM)."""
+    L = mx.lib()
+    Q4K, Q6K = int(mx.QuantType.Q4_K), int(mx.QuantType.Q6_K)
+    assert mx.workspace_size(Q4K, 1024, 4096, 1) == 0
+    assert mx.workspace_size(Q4K, 1024, 4096, 0) == 0
+    w = mx.workspace_size(Q4K, 1024, 4096, 512)
+    assert w > 0 and w % (4 * 512 * 1024) == 0
+
+    def grouped(specs, K, M):
+        arr = (qgemm.Item * len(specs))()
+        for i, (qt, N) in enumerate(specs):
+            arr[i] = qgemm.Item(qt, N, K, 0, None, None, 0, None, 2)
+        n = ctypes.c_size_t(7)
+        rc = L.mlxr_qgemm_grouped_workspace_size(len(specs), arr, M, ctypes.byref(n))
+        return rc, n.value
+
+    assert grouped([(Q4K, 4096), (Q4K, 1024), (Q4K, 1024)], 4096, 1) == (0, 0)
+    rc, b = grouped([(Q4K, 4096), (Q4K, 1024), (Q4K, 1024)], 4096, 512)
+    assert rc == 0 and b > 0 and b % (4 * 512 * 6144) == 0  # one launch over N = 6144
+    # a Q6_K item runs on its own: the need is the larger of the two launches
+    rc, b2 = grouped([(Q4K, 4096), (Q4K, 1024), (Q6K, 1024)], 4096, 512)
+    single = mx.workspace_size(Q6K, 1024, 4096, 512)
+    assert rc == 0 and b2 >= single
+    assert grouped([(Q4K, 4096), (Q4K, 1024)], 2048, 512)[0] == 0
+    rc, _ = grouped([(Q4K, 4096), (Q4K, 1000)], 4096, 512)
+    assert rc == 0
+    arr = (qgemm.Item * 2)(qgemm.Item(Q4K, 4096, 4096, 0, None, None, 0, None, 2),
+                           qgemm.Item(Q4K, 4096, 2048, 0, None, None, 0, None, 2))
+    n = ctypes.c_size_t(0)
+    assert L.mlxr_qgemm_grouped_workspace_size(2, arr, 512, ctypes.byref(n)) == -3  # K differs
