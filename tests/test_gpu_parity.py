@@ -243,6 +243,27 @@ def test_grouped_tiled_launches(cuda, M, K):
         assert orc.normwise_rel_err(y.cpu().numpy(), ref) <= TOL, i
 
 
+def test_grouped_tiled_many_items_f16(cuda):
+    """Five same-type weights (more than one launch holds: four, then one), fp16 activations
+    and outputs, a K that ends on a half step (Q8_0, K % 64 == 32), with and without the
+    workspace."""
+    import torch
+    M, K = 100, 1056
+    Ns = [256, 100, 384, 64, 520]
+    gg = [mx.synth_gguf(Q80, N, K, 400 + i) for i, N in enumerate(Ns)]
+    ws = [mx.pack_weights(g, N, K, Q80, device=cuda) for g, N in zip(gg, Ns)]
+    x, xf = _act(torch, M, K, mx.F16, 410, cuda)
+    for use_ws in (False, True):
+        ys = mx.q_gemm_dequant_grouped(x, ws, out_dtype=torch.float16, workspace=use_ws)
+        for i, (w, y) in enumerate(zip(ws, ys)):
+            ref = orc.gemm_f64(int(Q80), M, w.N, K, gg[i], xf)
+            assert orc.normwise_rel_err(y.float().cpu().numpy(), ref) <= TOL, (use_ws, i)
+            if not use_ws:
+                y1 = mx.q_gemm_dequant(x, w, M, w.N, K, Q80, out_dtype=torch.float16)
+                if mx.workspace_size(Q80, w.N, K, M) == 0:  # the separate call is unsplit too
+                    assert torch.equal(y, y1), i
+
+
 @pytest.mark.parametrize("qt,M,N,K", [(Q4K, 300, 512, 4096), (Q6K, 256, 256, 2048), (Q80, 130, 384, 1056),
                                       (Q4K, 64, 1024, 14336)])
 def test_mfma_few_tiles_long_k(cuda, qt, M, N, K):
