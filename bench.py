@@ -19,6 +19,7 @@ launch overhead is not in their figures.)
   c5  Llama-3-70B layer, Q4_K + Q6_K (v, down), 7 GEMMs in a hipGraph at M=1 and M=256,
       grouped as a decoder layer issues them (5 launches, plus split-K reduces at M=256)
   mlp (extra) Llama-3-8B gate/up + SwiGLU gating at M=1, fused vs grouped + gating kernel
+  lmhead (extra) Llama-3-8B output head as Q6_K GEMV at M=1 (N = 128256)
 The CPU baseline is the reference's CPU path (dequantize all of W to fp32, then the naive
 fp32 loop; restated in oracle/orc.c) on the headline workload, one thread.
 
@@ -55,7 +56,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="headline,c1,c3,c4,c5,mlp")
+    ap.add_argument("--only", default="headline,c1,c3,c4,c5,mlp,lmhead")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--skip-dropin", action="store_true",
                     help="do not time the seven-call drop-in step (profiler runs of the headline kernel)")
@@ -419,6 +420,23 @@ def run_mlp(cx, args):
     return res
 
 
+def run_lmhead(cx, args):
+    """Llama-3-8B lm_head as Q6_K (the Q4_K_M layout keeps the output head in Q6_K): GEMV at
+    M=1, N = 128256 (vocabulary), K = 4096; 431 MB of weights, over two packed copies so
+    consecutive calls stream from HBM.  Not a BASELINE config."""
+    mx, torch = cx.mx, cx.torch
+    N, K = 128256, 4096
+    _, copies, _ = pack_copies(cx, [("head", N, K, Q6K)], SEED_BASE + 7, min_copies=2)
+    x = cx.act(1, K, mx.BF16, SEED_BASE + 7001)
+    y = torch.empty((1, N), dtype=torch.bfloat16, device=cx.dev)
+    fn = lambda r: mx.q_gemm_dequant(x, copies[r % len(copies)]["head"], 1, N, K, Q6K, out=y, path=mx.PATH_GEMV)
+    fn(0)
+    us = 1e3 * cx.graph_ms(fn, 2 * len(copies))
+    b = gemm_bytes(mx, Q6K, 1, N, K)
+    return {"shape": "M=1 N=128256 K=4096 Q6_K, x/y bf16", "us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 def run_c5(cx, args):
     mx, torch = cx.mx, cx.torch
     _, copies, layer = pack_copies(cx, LLAMA3_70B, SEED_BASE + 4, min_copies=2)
@@ -489,7 +507,8 @@ def main():
         run_headline(cx, args, out)
     configs = {}
     for key, fn in (("c1_q8_0_gemv_tinyllama", run_c1), ("c3_q4k_skinny", run_c3), ("c4_q4k_prefill", run_c4),
-                    ("c5_llama3_70b_layer_graph", run_c5), ("mlp_swiglu_m1", run_mlp)):
+                    ("c5_llama3_70b_layer_graph", run_c5), ("mlp_swiglu_m1", run_mlp),
+                    ("lmhead_q6k_llama3_8b_m1", run_lmhead)):
         if key.split("_")[0] in only:
             configs[key] = fn(cx, args)
             torch.cuda.empty_cache()

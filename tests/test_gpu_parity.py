@@ -109,6 +109,19 @@ MFMA_CASES = [
 ]
 
 
+def test_gemv_lm_head_q6k_full_size(cuda):
+    """The Llama-3-8B output head as Q6_K (N = 128256 rows, K = 4096) at M = 1: every row
+    against the fp64 oracle."""
+    import torch
+    N, K = 128256, 4096
+    w, pw = _packed(torch, Q6K, N, K, 91, cuda)
+    x, xf = _act(torch, 1, K, mx.BF16, 92, cuda)
+    y = mx.q_gemm_dequant(x, pw, 1, N, K, Q6K, out_dtype=torch.float32)
+    ref = orc.gemm_f64(int(Q6K), 1, N, K, w, xf)
+    err = orc.normwise_rel_err(y.cpu().numpy(), ref)
+    assert err <= 3e-5, err
+
+
 @pytest.mark.parametrize("qt,M,N,K", MFMA_CASES)
 def test_mfma_matches_oracle(cuda, qt, M, N, K):
     import torch
