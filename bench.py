@@ -135,6 +135,17 @@ def gemm_bytes(mx, qt, M, N, K, xsz=2, ysz=2):
 
 # ------------------------------------------------------------------------------ headline
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def run_headline(cx, args, out):
     mx, torch = cx.mx, cx.torch
     specs = [(n, N, K, Q4K) for n, N, K in LLAMA3_8B]
@@ -272,7 +283,7 @@ def run_headline(cx, args, out):
             "sample": "the full headline step (Llama-3-8B Q4_K q,k,v,o,gate,up,down at M=1) through the "
                       "reference eval_cpu restated in oracle/orc.c: fp32 dequant of all of W, then the naive "
                       "fp32 loop; 1 thread; median of 3 runs",
-            "seconds_per_step": round(sec, 4)}
+            "seconds_per_step": round(sec, 4), "cpu_model": cpu_model()}
         # "MLX-CPU-class" baseline: the same fp32 dequant on every core of this process's
         # CPU share (OpenMP over rows), then a BLAS fp32 GEMV (torch on the host)
         cores = min(len(os.sched_getaffinity(0)), 16)
@@ -298,6 +309,7 @@ def run_headline(cx, args, out):
         dq, mm = float(np.median(dq_runs)), float(np.median(mm_runs))
         out["cpu_baseline_all_cores"] = {
             "value": round(step_bytes / (dq + mm) / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
             "kind": "port", "dequant_s": round(dq, 4), "matmul_s": round(mm, 4),
             "sample": "the full headline step: oracle fp32 dequant (OpenMP) + host BLAS fp32 GEMV "
                       "(torch.matmul), all cores of the process's CPU share; median of 3 runs"}
