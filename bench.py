@@ -272,7 +272,7 @@ def run_headline(cx, args, out):
         xf = {k: orc.bf16_bits_to_f32(v.view(torch.int16).cpu().numpy().view(np.uint16)).reshape(1, -1)
               for k, v in x.items()}
         runs = []
-        for _ in range(3):
+        for _ in range(5):
             t = time.perf_counter()
             for n, N, K in LLAMA3_8B:
                 orc.eval_cpu(Q4K, 1, N, K, gguf[n], xf[K])
@@ -282,7 +282,7 @@ def run_headline(cx, args, out):
             "value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": "the full headline step (Llama-3-8B Q4_K q,k,v,o,gate,up,down at M=1) through the "
                       "reference eval_cpu restated in oracle/orc.c: fp32 dequant of all of W, then the naive "
-                      "fp32 loop; 1 thread; median of 3 runs",
+                      "fp32 loop; 1 thread; median of 5 runs",
             "seconds_per_step": round(sec, 4), "cpu_model": cpu_model()}
         # "MLX-CPU-class" baseline: the same fp32 dequant on every core of this process's
         # CPU share (OpenMP over rows), then a BLAS fp32 GEMV (torch on the host)
@@ -292,7 +292,7 @@ def run_headline(cx, args, out):
         torch.set_num_threads(cores)
         xt = {k: torch.from_numpy(v) for k, v in xf.items()}
         dq_runs, mm_runs = [], []
-        for _ in range(3):
+        for _ in range(5):
             tdq = tmm = 0.0
             for n, N, K in LLAMA3_8B:
                 t = time.perf_counter()
@@ -312,7 +312,7 @@ def run_headline(cx, args, out):
             "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
             "kind": "port", "dequant_s": round(dq, 4), "matmul_s": round(mm, 4),
             "sample": "the full headline step: oracle fp32 dequant (OpenMP) + host BLAS fp32 GEMV "
-                      "(torch.matmul), all cores of the process's CPU share; median of 3 runs"}
+                      "(torch.matmul), all cores of the process's CPU share; median of 5 runs"}
     del graphs, graphs7, copies
     torch.cuda.empty_cache()
 
