@@ -280,7 +280,7 @@ def run_headline(cx, args, out):
         sec = float(np.median(runs))
         out["cpu_baseline"] = {
             "value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "the full headline step (Llama-3-8B Q4_K q,k,v,o,gate,up,down at M=1) through the "
+            "sample": "one layer of the headline step (Llama-3-8B Q4_K q,k,v,o,gate,up,down at M=1) through the "
                       "reference eval_cpu restated in oracle/orc.c: fp32 dequant of all of W, then the naive "
                       "fp32 loop; 1 thread; median of 5 runs",
             "seconds_per_step": round(sec, 4), "cpu_model": cpu_model()}
@@ -311,7 +311,7 @@ def run_headline(cx, args, out):
             "value": round(step_bytes / (dq + mm) / 1e9, 3), "unit": "GB/s", "cores": cores,
             "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
             "kind": "port", "dequant_s": round(dq, 4), "matmul_s": round(mm, 4),
-            "sample": "the full headline step: oracle fp32 dequant (OpenMP) + host BLAS fp32 GEMV "
+            "sample": "one layer of the headline step: oracle fp32 dequant (OpenMP) + host BLAS fp32 GEMV "
                       "(torch.matmul), all cores of the process's CPU share; median of 5 runs"}
     del graphs, graphs7, copies
     torch.cuda.empty_cache()
