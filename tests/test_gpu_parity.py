@@ -106,6 +106,8 @@ MFMA_CASES = [
     # one wavefront per workgroup (short K) with two M-blocks: every row must be stored
     (Q4K, 40, 64, 256), (Q6K, 64, 32, 512), (Q80, 33, 64, 64),
     (Q5K, 128, 256, 1024), (Q5K, 9, 96, 768), (Q5K, 300, 200, 2048),
+    # the skinny kernel's narrow variant with one and two 16-row activation blocks
+    (Q6K, 12, 200, 512), (Q6K, 24, 96, 768), (Q80, 30, 64, 1056), (Q40, 17, 130, 96), (Q5K, 32, 64, 256),
 ]
 
 
