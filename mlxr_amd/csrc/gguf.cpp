@@ -5,7 +5,8 @@
 // Follows the file format the reference reads in daemon/registry/gguf_parser.cpp
 // (read_header :318-337, read_string :339-352, read_metadata_value :354-426,
 // read_metadata :428-446, read_tensor_infos :448-491, data offset :306-313) and the
-// mmap view of core/runtime/mmap_loader.cpp:102-199, with the fixes listed in the header
+// mmap view of core/runtime/mmap_loader.cpp:102-199 (WILLNEED advice before an upload as
+// advise(), :243-278), with the fixes listed in the header
 // (GGUF block sizes, general.alignment, bounds-checked reads).
 #include <fcntl.h>
 #include <hip/hip_runtime.h>
@@ -478,6 +479,14 @@ int mlxr_gguf_upload(const mlxr_gguf* g, uint64_t i, void* packed_dev, void* str
     return set_error(MLXR_E_INVALID, "tensor %s: data range [%llu, +%llu) is outside the %llu-byte file", t.name,
                      (unsigned long long)t.file_offset, (unsigned long long)t.size,
                      (unsigned long long)g->hdr.file_size);
+  if (g->map) {
+    // the pack reads the tensor once, front to back: ask for its pages ahead of the copy
+    // (as the reference's WILLNEED advice on a mapped region; advisory, errors ignored)
+    const uintptr_t pg = (uintptr_t)sysconf(_SC_PAGESIZE);
+    const uintptr_t a = (uintptr_t)t.data & ~(pg - 1);
+    const uintptr_t e = ((uintptr_t)t.data + (uintptr_t)t.size + pg - 1) & ~(pg - 1);
+    (void)madvise((void*)a, (size_t)(e - a), MADV_WILLNEED);
+  }
   return mlxr_qgemm_pack(qt, (int)t.dims[1], (int)t.dims[0], t.data, packed_dev, stream);
 }
 
