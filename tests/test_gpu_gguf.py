@@ -17,7 +17,10 @@ def test_gguf_upload_matches_pack(cuda, tmp_path):
     T = gguf.GGMLType
     specs = [("blk.0.attn_q.weight", T.Q4_K, mx.QuantType.Q4_K, 256, 1024),
              ("blk.0.attn_v.weight", T.Q6_K, mx.QuantType.Q6_K, 128, 512),
-             ("blk.0.ffn_down.weight", T.Q8_0, mx.QuantType.Q8_0, 96, 1056)]
+             ("blk.0.ffn_down.weight", T.Q8_0, mx.QuantType.Q8_0, 96, 1056),
+             ("blk.1.attn_q.weight", T.Q4_0, mx.QuantType.Q4_0, 64, 544),
+             ("blk.1.attn_k.weight", T.Q4_1, mx.QuantType.Q4_1, 80, 256),
+             ("blk.1.ffn_up.weight", T.Q5_K, mx.QuantType.Q5_K, 72, 768)]
     w = gw.Writer(3, alignment=64)
     w.add("general.architecture", gw.STR, "llama")
     blocks = {}
