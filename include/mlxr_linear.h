@@ -8,9 +8,11 @@
 // beside it); the weight is held as packed GGUF blocks in device memory instead of an MLX
 // float tensor.  forward() takes and returns device arrays (bf16 or fp16 activations,
 // output in the input dtype) and runs on the given HIP stream; it is stream-ordered and
-// allocates only its output (plus a split-K workspace the first time a large M needs one,
-// kept by the layer).  One layer must not run forward on two streams at once (the
-// workspace is per layer).  Errors throw std::runtime_error, as the reference does.
+// never synchronises.  The allocating forward() uses stream-ordered allocations
+// (hipMallocAsync / hipFreeAsync) for its output and temporaries; the forward() overloads
+// with caller-owned outputs and workspace allocate nothing.  One layer must not run the
+// allocating forward on two streams at once (its split-K workspace is per layer).  Errors
+// throw std::runtime_error, as the reference does.
 #pragma once
 
 #include <string>
@@ -35,8 +37,16 @@ class Linear {
   // Bias [out_features] on the device (fp32, fp16 or bf16).  Only for layers built with bias.
   void set_bias(const kernels::array& bias);
 
-  // x [..., in_features] -> [..., out_features], M = product of the leading dims.
+  // x [..., in_features] -> [..., out_features], M = product of the leading dims.  The
+  // output (and a split-K workspace kept by the layer) are stream-ordered allocations on s.
   kernels::array forward(const kernels::array& x, kernels::Stream s = {});
+  // Same into the caller's y (M * out_features elements of float32, float16 or bfloat16)
+  // with the caller's workspace (NULL / too small: unsplit): allocates nothing and never
+  // synchronises, so it can be captured into a HIP graph.
+  void forward(const kernels::array& x, kernels::array& y, void* workspace, size_t workspace_bytes,
+               kernels::Stream s = {});
+  // Workspace bytes forward() can use at M rows (0: none needed).
+  size_t workspace_size(int M) const;
 
   const kernels::array& weight() const { return weight_; }
   const kernels::array* bias() const { return has_bias_ ? &bias_ : nullptr; }
@@ -45,7 +55,7 @@ class Linear {
 
  private:
   friend class MLP;
-  void run(const kernels::array& x, int M, kernels::array& y, kernels::Stream s);
+  void run(const kernels::array& x, int M, kernels::array& y, void* ws, size_t ws_bytes, kernels::Stream s);
   int in_features_, out_features_;
   bool has_bias_;
   kernels::array weight_;  // Dtype::packed
@@ -54,14 +64,22 @@ class Linear {
 };
 
 // SwiGLU MLP (reference layers.cpp:383-414): down(swish(gate(x)) * up(x)).  gate, up and
-// the gating run as mlxr_qgemm_swiglu: one launch for M <= 4.
+// the gating run as mlxr_qgemm_swiglu: one launch (plus a split-K reduce where it splits).
 class MLP {
  public:
   MLP(int hidden_size, int intermediate_size);
   Linear& gate_proj() { return gate_; }
   Linear& up_proj() { return up_; }
   Linear& down_proj() { return down_; }
+  // x [..., hidden] -> [..., hidden]; h and the workspace are stream-ordered temporaries.
   kernels::array forward(const kernels::array& x, kernels::Stream s = {});
+  // Same into the caller's y ([..., hidden], x's dtype) with the caller's h ([M,
+  // intermediate] in x's dtype: swish(gate) * up) and workspace (workspace_size bytes;
+  // NULL / smaller: unsplit launches, except for operands of 2 GiB or more, which need it):
+  // allocates nothing and never synchronises (HIP-graph capturable).
+  void forward(const kernels::array& x, kernels::array& y, kernels::array& h, void* workspace,
+               size_t workspace_bytes, kernels::Stream s = {});
+  size_t workspace_size(int M, kernels::Dtype dtype = kernels::Dtype::bfloat16) const;
 
  private:
   int hidden_, inter_;

@@ -41,8 +41,12 @@ struct Stream {
 class array {
  public:
   array() = default;
-  // Allocates nbytes(shape, dtype) of device memory.
+  // Allocates nbytes(shape, dtype) of device memory (hipMalloc; freed with hipFree).
   array(std::vector<int> shape, Dtype dtype);
+  // Stream-ordered allocation on s (hipMallocAsync; freed with hipFreeAsync on s when the
+  // last owner lets go): no device synchronisation either way.  Use it on s only (other
+  // streams must be ordered after s's work by the caller).
+  array(std::vector<int> shape, Dtype dtype, Stream s);
   // Wraps memory the caller owns (not freed by the array).
   static array borrow(void* dev_ptr, std::vector<int> shape, Dtype dtype);
 
@@ -62,7 +66,7 @@ class array {
 
  private:
   friend array pack_weights(const void*, int, int, QuantType, Stream);
-  friend array pack_weights_device(const array&, int, int, QuantType, Stream);
+  friend array pack_weights_device(const array&, int, int, QuantType, Stream, bool);
   std::shared_ptr<void> ptr_;
   std::vector<int> shape_;
   Dtype dtype_ = Dtype::uint8;
@@ -80,7 +84,10 @@ class QGemmDequantPrimitive {
   // There is no CPU implementation in this library: throws std::runtime_error.
   void eval_cpu(const std::vector<array>& inputs, std::vector<array>& outputs);
   // inputs = {input [M,K] bf16/fp16, weights (packed, or raw GGUF uint8 on device), bias [N]?}
-  // outputs = {out [M,N]} (allocated here if empty, dtype of the input).
+  // outputs = {out [M,N]} (allocated stream-ordered here if empty, dtype of the input; a
+  // caller's output must hold M*N elements of its dtype).  Raw GGUF weights are packed
+  // into a stream-ordered temporary for the call (no synchronisation); pass weights
+  // packed once by pack_weights() to avoid that per-call pack.
   void eval_gpu(const std::vector<array>& inputs, std::vector<array>& outputs);
 
   std::vector<std::vector<int>> output_shapes(const std::vector<array>&) const { return {{M_, N_}}; }
@@ -111,8 +118,10 @@ array q_gemm_dequant(const array& input, const array& weights, int M, int N, int
 
 // One-time upload of GGUF blocks from host memory into the packed device layout.
 array pack_weights(const void* gguf_host, int N, int K, QuantType quant_type, Stream s = {});
-// Same, from GGUF bytes already on the device (Dtype::uint8 array).
-array pack_weights_device(const array& gguf_dev, int N, int K, QuantType quant_type, Stream s = {});
+// Same, from GGUF bytes already on the device (Dtype::uint8 array); stream_ordered
+// allocates the packed array on s (hipMallocAsync, see array).
+array pack_weights_device(const array& gguf_dev, int N, int K, QuantType quant_type, Stream s = {},
+                          bool stream_ordered = false);
 
 size_t compute_quantized_weight_size(int N, int K, QuantType quant_type);
 const char* quant_type_name(QuantType type);

@@ -11,9 +11,8 @@ namespace mlxr {
 
 namespace {
 
-// silu(g) * u in fp32; silu(g) = g / (1 + exp(-g)) (exp saturates to inf for g < -88,
-// giving -0 or 0 as the limit requires).
-__device__ __forceinline__ float swiglu1(float g, float u) { return g / (1.f + __expf(-g)) * u; }
+// swiglu1 (qgemm_device.h): silu(g) * u in fp32, silu(g) = g / (1 + exp(-g)) (exp
+// saturates to inf for g < -88, giving -0 or 0 as the limit requires).
 
 template <int DT>
 __global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ gate, const void* __restrict__ up,

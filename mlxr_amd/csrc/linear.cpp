@@ -4,7 +4,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <stdexcept>
+#include <string>
 
 #include "../../include/mlxr_qgemm.h"
 
@@ -57,39 +59,55 @@ void Linear::set_bias(const kernels::array& bias) {
   bias_ = bias;
 }
 
-void Linear::run(const kernels::array& x, int M, kernels::array& y, kernels::Stream s) {
+size_t Linear::workspace_size(int M) const {
+  if (weight_.dtype() != kernels::Dtype::packed) throw std::runtime_error("Linear: weight not loaded");
+  size_t ws = 0;
+  check(mlxr_qgemm_workspace_size((int)weight_.quant_type(), out_features_, in_features_, M, &ws));
+  return ws;
+}
+
+void Linear::run(const kernels::array& x, int M, kernels::array& y, void* ws, size_t ws_bytes, kernels::Stream s) {
   if (weight_.dtype() != kernels::Dtype::packed) throw std::runtime_error("Linear: weight not loaded");
   if (has_bias_ && bias_.nbytes() == 0) throw std::runtime_error("Linear: bias not set");
+  if (y.nbytes() < (size_t)M * (size_t)out_features_ * kernels::dtype_size(y.dtype()))
+    throw std::runtime_error("Linear: output buffer is smaller than [M, out_features]");
   const int qt = (int)weight_.quant_type();
-  size_t ws = 0;
-  check(mlxr_qgemm_workspace_size(qt, out_features_, in_features_, M, &ws));
-  if (ws > 0x7fffffffu) ws = 0;  // beyond one array: run unsplit
-  if (ws > workspace_.nbytes()) {
-    // the previous workspace may still be in use by queued work on this stream
-    if (workspace_.nbytes()) {
-      const hipError_t e = hipStreamSynchronize((hipStream_t)s.hip_stream);
-      if (e != hipSuccess) throw std::runtime_error(hipGetErrorString(e));
-    }
-    workspace_ = kernels::array({(int)ws}, kernels::Dtype::uint8);
-  }
   check(mlxr_qgemm_run_ws(qt, out_features_, in_features_, 0, weight_.data<void>(), x.data<void>(),
                           dt_code(x.dtype()), has_bias_ ? bias_.data<void>() : nullptr,
                           has_bias_ ? dt_code(bias_.dtype()) : MLXR_F32, y.data<void>(), dt_code(y.dtype()), M,
-                          MLXR_PATH_AUTO, workspace_.nbytes() ? workspace_.data<void>() : nullptr,
-                          workspace_.nbytes(), s.hip_stream));
+                          MLXR_PATH_AUTO, ws_bytes ? ws : nullptr, ws ? ws_bytes : 0, s.hip_stream));
+}
+
+namespace {
+long rows_of(const kernels::array& x, int features, const char* what) {
+  if (x.ndim() < 1 || x.shape(-1) != features) throw std::runtime_error(std::string("Input shape must be [..., ") + what + "]");
+  if (x.dtype() != kernels::Dtype::bfloat16 && x.dtype() != kernels::Dtype::float16)
+    throw std::runtime_error("layer input must be bfloat16 or float16");
+  long M = 1;
+  for (int d = 0; d + 1 < x.ndim(); ++d) M *= x.shape(d);
+  if (M > 0x7fffffffL) throw std::runtime_error("layer input: too many rows");
+  return M;
+}
+}  // namespace
+
+void Linear::forward(const kernels::array& x, kernels::array& y, void* workspace, size_t workspace_bytes,
+                     kernels::Stream s) {
+  const long M = rows_of(x, in_features_, "in_features");
+  if (M > 0) run(x, (int)M, y, workspace, workspace_bytes, s);
 }
 
 kernels::array Linear::forward(const kernels::array& x, kernels::Stream s) {
-  if (x.ndim() < 1 || x.shape(-1) != in_features_) throw std::runtime_error("Input shape must be [..., in_features]");
-  if (x.dtype() != kernels::Dtype::bfloat16 && x.dtype() != kernels::Dtype::float16)
-    throw std::runtime_error("Linear input must be bfloat16 or float16");
-  long M = 1;
-  for (int d = 0; d + 1 < x.ndim(); ++d) M *= x.shape(d);
-  if (M > 0x7fffffffL) throw std::runtime_error("Linear: too many rows");
+  const long M = rows_of(x, in_features_, "in_features");
   std::vector<int> shape = x.shape();
   shape.back() = out_features_;
-  kernels::array y(shape, x.dtype());
-  if (M > 0) run(x, (int)M, y, s);
+  kernels::array y(shape, x.dtype(), s);
+  if (M > 0) {
+    size_t ws = workspace_size((int)M);
+    if (ws > 0x7fffffffu) ws = 0;  // beyond one array: run unsplit
+    // grown on demand; the old workspace is released in stream order after queued work
+    if (ws > workspace_.nbytes()) workspace_ = kernels::array({(int)ws}, kernels::Dtype::uint8, s);
+    run(x, (int)M, y, workspace_.nbytes() ? workspace_.data<void>() : nullptr, workspace_.nbytes(), s);
+  }
   return y;
 }
 
@@ -100,32 +118,48 @@ MLP::MLP(int hidden_size, int intermediate_size)
       up_(hidden_size, intermediate_size, false),
       down_(intermediate_size, hidden_size, false) {}
 
-kernels::array MLP::forward(const kernels::array& x, kernels::Stream s) {
-  if (x.ndim() < 1 || x.shape(-1) != hidden_) throw std::runtime_error("Input shape must be [..., hidden_size]");
-  if (x.dtype() != kernels::Dtype::bfloat16 && x.dtype() != kernels::Dtype::float16)
-    throw std::runtime_error("MLP input must be bfloat16 or float16");
+size_t MLP::workspace_size(int M, kernels::Dtype dtype) const {
   if (gate_.weight_.dtype() != kernels::Dtype::packed || up_.weight_.dtype() != kernels::Dtype::packed)
     throw std::runtime_error("MLP: gate/up weights not loaded");
-  long M = 1;
-  for (int d = 0; d + 1 < x.ndim(); ++d) M *= x.shape(d);
+  size_t ws = 0;
+  check(mlxr_qgemm_swiglu_workspace_size((int)gate_.weight_.quant_type(), inter_, hidden_, M, dt_code(dtype), &ws));
+  return std::max(ws, down_.workspace_size(M));
+}
+
+void MLP::forward(const kernels::array& x, kernels::array& y, kernels::array& h, void* workspace,
+                  size_t workspace_bytes, kernels::Stream s) {
+  const long M = rows_of(x, hidden_, "hidden_size");
+  if (gate_.weight_.dtype() != kernels::Dtype::packed || up_.weight_.dtype() != kernels::Dtype::packed)
+    throw std::runtime_error("MLP: gate/up weights not loaded");
+  const int qt = (int)gate_.weight_.quant_type();
+  if (qt != (int)up_.weight_.quant_type()) throw std::runtime_error("MLP: gate and up must share a quant type");
+  if (h.dtype() != x.dtype() || h.nbytes() < (size_t)M * (size_t)inter_ * kernels::dtype_size(x.dtype()))
+    throw std::runtime_error("MLP: h must hold [M, intermediate_size] in the input dtype");
+  if (M == 0) return;
+  const int dt = dt_code(x.dtype());
+  // gate, up and the gating: one launch (the fused kernels) for every M whose operands
+  // stay below 2 GiB; the workspace holds split-K partials, or up when unfused
+  check(mlxr_qgemm_swiglu(qt, inter_, hidden_, gate_.weight_.data<void>(), up_.weight_.data<void>(), x.data<void>(),
+                          dt, h.data<void>(), dt, (int)M, workspace_bytes ? workspace : nullptr,
+                          workspace ? workspace_bytes : 0, s.hip_stream));
   std::vector<int> hshape = x.shape();
   hshape.back() = inter_;
-  kernels::array g(hshape, x.dtype());
-  if (M > 0) {
-    const int qt = (int)gate_.weight_.quant_type();
-    if (qt != (int)up_.weight_.quant_type()) throw std::runtime_error("MLP: gate and up must share a quant type");
-    const int dt = dt_code(x.dtype());
-    size_t ws = 0;
-    check(mlxr_qgemm_swiglu_workspace_size(qt, inter_, hidden_, (int)M, dt, &ws));
-    kernels::array u;
-    if (ws) u = kernels::array({(int)ws}, kernels::Dtype::uint8);
-    // M <= 4: gate, up and the gating in one launch; above, up goes to u
-    check(mlxr_qgemm_swiglu(qt, inter_, hidden_, gate_.weight_.data<void>(), up_.weight_.data<void>(),
-                            x.data<void>(), dt, g.data<void>(), dt, (int)M, ws ? u.data<void>() : nullptr, ws,
-                            s.hip_stream));
-  }
-  kernels::array y = down_.forward(g, s);
-  // the temporaries are freed here (hipFree waits for the device), after the queued kernels
+  const kernels::array hv = kernels::array::borrow(h.data<void>(), hshape, x.dtype());
+  down_.forward(hv, y, workspace, workspace_bytes, s);
+}
+
+kernels::array MLP::forward(const kernels::array& x, kernels::Stream s) {
+  const long M = rows_of(x, hidden_, "hidden_size");
+  std::vector<int> hshape = x.shape();
+  hshape.back() = inter_;
+  kernels::array h(hshape, x.dtype(), s);
+  kernels::array y(x.shape(), x.dtype(), s);
+  size_t ws = M > 0 ? workspace_size((int)M, x.dtype()) : 0;
+  if (ws > 0x7fffffffu) throw std::runtime_error("MLP: workspace of 2 GiB or more");
+  kernels::array w;
+  if (ws) w = kernels::array({(int)ws}, kernels::Dtype::uint8, s);
+  forward(x, y, h, ws ? w.data<void>() : nullptr, ws, s);
+  // h and w are released in stream order (hipFreeAsync) after the queued kernels
   return y;
 }
 

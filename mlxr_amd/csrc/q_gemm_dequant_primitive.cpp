@@ -48,6 +48,19 @@ array::array(std::vector<int> shape, Dtype dtype) : shape_(std::move(shape)), dt
   });
 }
 
+array::array(std::vector<int> shape, Dtype dtype, Stream s) : shape_(std::move(shape)), dtype_(dtype) {
+  nbytes_ = elems(shape_) * dtype_size(dtype_);
+  void* p = nullptr;
+  hipStream_t hs = (hipStream_t)s.hip_stream;
+  if (nbytes_) {
+    const hipError_t e = hipMallocAsync(&p, nbytes_, hs);
+    if (e != hipSuccess) throw std::runtime_error(std::string("hipMallocAsync failed: ") + hipGetErrorString(e));
+  }
+  ptr_ = std::shared_ptr<void>(p, [hs](void* q) {
+    if (q) (void)hipFreeAsync(q, hs);
+  });
+}
+
 array array::borrow(void* dev_ptr, std::vector<int> shape, Dtype dtype) {
   array a;
   a.shape_ = std::move(shape);
@@ -119,30 +132,38 @@ void QGemmDequantPrimitive::eval_gpu(const std::vector<array>& inputs, std::vect
       throw std::runtime_error("packed weights do not match (quant_type, N, K)");
     packed = weights;
   } else {
-    // Raw GGUF blocks on the device, as the reference passes them: pack for this call.
+    // Raw GGUF blocks on the device, as the reference passes them: pack for this call into
+    // a stream-ordered temporary, released (hipFreeAsync) after the GEMM in stream order.
     if (weights.nbytes() < compute_quantized_weight_size(N_, K_, quant_type_))
       throw std::runtime_error("weights buffer is smaller than N * K/group * sizeof(block)");
-    packed = pack_weights_device(weights, N_, K_, quant_type_, stream_);
+    packed = pack_weights_device(weights, N_, K_, quant_type_, stream_, true);
   }
   if (outputs.empty()) outputs.emplace_back();
-  if (outputs[0].nbytes() == 0) outputs[0] = array({M_, N_}, input.dtype());
+  if (outputs[0].nbytes() == 0) outputs[0] = array({M_, N_}, input.dtype(), stream_);
   array& out = outputs[0];
+  if (out.dtype() != Dtype::float32 && out.dtype() != Dtype::float16 && out.dtype() != Dtype::bfloat16)
+    throw std::runtime_error("QGemmDequant output must be float32, float16 or bfloat16");
+  if (out.nbytes() < (size_t)M_ * (size_t)N_ * dtype_size(out.dtype()))
+    throw std::runtime_error("QGemmDequant output buffer is smaller than [M, N]");
   const int ydt = out.dtype() == Dtype::float32 ? MLXR_F32 : out.dtype() == Dtype::float16 ? MLXR_F16 : MLXR_BF16;
   int bdt = MLXR_F32;
   if (bias) bdt = bias->dtype() == Dtype::float32 ? MLXR_F32 : bias->dtype() == Dtype::float16 ? MLXR_F16 : MLXR_BF16;
   check(mlxr_qgemm_run((int)quant_type_, N_, K_, group_size_, packed.data<void>(), input.data<void>(), xdt,
                        bias ? bias->data<void>() : nullptr, bdt, out.data<void>(), ydt, M_, stream_.hip_stream));
-  if (weights.dtype() != Dtype::packed) {
-    // the temporary packed buffer must outlive the kernel
-    const hipError_t e = hipStreamSynchronize((hipStream_t)stream_.hip_stream);
-    if (e != hipSuccess) throw std::runtime_error(hipGetErrorString(e));
-  }
 }
 
-array pack_weights(const void* gguf_host, int N, int K, QuantType quant_type, Stream s) {
+namespace {
+// Packed buffers are one-dimensional uint8 arrays: their byte count must fit the shape.
+int packed_bytes(int N, int K, QuantType quant_type) {
   size_t bytes = 0;
   check(mlxr_qgemm_packed_size((int)quant_type, N, K, &bytes));
-  array a({(int)bytes}, Dtype::uint8);
+  if (bytes > 0x7fffffffu) throw std::runtime_error("packed weight of 2 GiB or more: split it by rows");
+  return (int)bytes;
+}
+}  // namespace
+
+array pack_weights(const void* gguf_host, int N, int K, QuantType quant_type, Stream s) {
+  array a({packed_bytes(N, K, quant_type)}, Dtype::uint8);
   check(mlxr_qgemm_pack((int)quant_type, N, K, gguf_host, a.data<void>(), s.hip_stream));
   a.dtype_ = Dtype::packed;
   a.qtype_ = quant_type;
@@ -151,10 +172,9 @@ array pack_weights(const void* gguf_host, int N, int K, QuantType quant_type, St
   return a;
 }
 
-array pack_weights_device(const array& gguf_dev, int N, int K, QuantType quant_type, Stream s) {
-  size_t bytes = 0;
-  check(mlxr_qgemm_packed_size((int)quant_type, N, K, &bytes));
-  array a({(int)bytes}, Dtype::uint8);
+array pack_weights_device(const array& gguf_dev, int N, int K, QuantType quant_type, Stream s, bool stream_ordered) {
+  const int bytes = packed_bytes(N, K, quant_type);
+  array a = stream_ordered ? array({bytes}, Dtype::uint8, s) : array({bytes}, Dtype::uint8);
   check(mlxr_qgemm_pack_device((int)quant_type, N, K, gguf_dev.data<void>(), a.data<void>(), s.hip_stream));
   a.dtype_ = Dtype::packed;
   a.qtype_ = quant_type;
@@ -172,7 +192,7 @@ array q_gemm_dequant(const array& input, const array& weights, int M, int N, int
   QGemmDequantPrimitive prim(s, M, N, K, quant_type, group_size, bias != nullptr);
   std::vector<array> inputs = {input, weights};
   if (bias) inputs.push_back(*bias);
-  std::vector<array> outputs = {array({M, N}, input.dtype())};
+  std::vector<array> outputs = {array({M, N}, input.dtype(), s)};
   prim.eval_gpu(inputs, outputs);
   return outputs[0];
 }

@@ -232,6 +232,8 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   return MLXR_OK;
 }
 
+}  // extern "C"
+
 namespace {
 
 // How a grouped call runs its items: launches of several items (GEMV at M <= 4, tiled MFMA
@@ -326,6 +328,8 @@ int run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int 
 
 }  // namespace
 
+extern "C" {
+
 int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,
                            void* stream) {
   return run_grouped(count, items, x_dev, x_dtype, M, nullptr, 0, stream);
@@ -361,6 +365,22 @@ int mlxr_qgemm_grouped_workspace_size(int count, const mlxr_qgemm_item* items, i
   return MLXR_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// How mlxr_qgemm_swiglu runs a shape: 0 GEMV launch (M <= 4), 1 narrow skinny kernel
+// (M <= 32), 2 tiled kernel, 3 unfused (operands of 2 GiB or more: two projections, then
+// mlxr_swiglu with up in the workspace).  Kinds 1 and 2 fuse the gating into the
+// projection launch; their workspace only holds split-K partials.
+int swiglu_kind(const mlxr::RunArgs& a) {
+  if (a.M <= kGemvMaxM && mlxr::gemv_groupable(a)) return 0;
+  if (!mlxr::mfma_groupable(a)) return 3;
+  return mlxr::skinny_swiglu_ok(a.M) ? 1 : 2;
+}
+}  // namespace
+
+extern "C" {
+
 int mlxr_qgemm_swiglu_workspace_size(int qtype, int N, int K, int M, int h_dtype, size_t* bytes) {
   mlxr::PackedLayout L;
   const int rc = check_type_shape(qtype, N, K, &L);
@@ -371,7 +391,12 @@ int mlxr_qgemm_swiglu_workspace_size(int qtype, int N, int K, int M, int h_dtype
   mlxr::RunArgs a;
   a.L = L;
   a.M = M;
-  *bytes = (M <= kGemvMaxM && mlxr::gemv_groupable(a)) ? 0 : (size_t)M * (size_t)N * (h_dtype == MLXR_F32 ? 4 : 2);
+  switch (M == 0 ? 0 : swiglu_kind(a)) {
+    case 1: *bytes = mlxr::skinny_swiglu_workspace_bytes(M, N, K); break;
+    case 2: *bytes = mlxr::mfma_swiglu_workspace_bytes(M, N, K); break;
+    case 3: *bytes = (size_t)M * (size_t)N * (h_dtype == MLXR_F32 ? 4 : 2); break;
+    default: *bytes = 0;
+  }
   return MLXR_OK;
 }
 
@@ -385,25 +410,35 @@ int mlxr_qgemm_swiglu(int qtype, int N, int K, const void* gate_packed, const vo
     return fail(MLXR_E_INVALID, "activation dtype must be BF16 or F16 (got %d)", x_dtype);
   if (M == 0) return MLXR_OK;
   if (!gate_packed || !up_packed || !x_dev || !h_dev) return fail(MLXR_E_INVALID, "null buffer");
-  if (need == 0) {
-    mlxr::RunArgs g, u;
-    mlxr::make_layout(qtype, N, K, &g.L);
-    u.L = g.L;
-    g.packed = (const uint8_t*)gate_packed;
-    u.packed = (const uint8_t*)up_packed;
-    g.x = u.x = x_dev;
-    g.x_dtype = u.x_dtype = x_dtype;
-    g.bias = u.bias = nullptr;
-    g.bias_dtype = u.bias_dtype = MLXR_F32;
-    g.y = h_dev;
-    u.y = nullptr;
-    g.y_dtype = u.y_dtype = h_dtype;
-    g.M = u.M = M;
-    const hipError_t e = mlxr::launch_gemv_swiglu(g, u, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e, "swiglu gemv launch");
-    return MLXR_OK;
+  mlxr::RunArgs g, u;
+  mlxr::make_layout(qtype, N, K, &g.L);
+  u.L = g.L;
+  g.packed = (const uint8_t*)gate_packed;
+  u.packed = (const uint8_t*)up_packed;
+  g.x = u.x = x_dev;
+  g.x_dtype = u.x_dtype = x_dtype;
+  g.bias = u.bias = nullptr;
+  g.bias_dtype = u.bias_dtype = MLXR_F32;
+  g.y = h_dev;
+  u.y = nullptr;
+  g.y_dtype = u.y_dtype = h_dtype;
+  g.M = u.M = M;
+  const int kind = swiglu_kind(g);
+  hipStream_t s = (hipStream_t)stream;
+  if (kind == 0) {
+    const hipError_t e = mlxr::launch_gemv_swiglu(g, u, s);
+    return e != hipSuccess ? hip_fail(e, "swiglu gemv launch") : MLXR_OK;
   }
-  // larger M: gate into h, up into the workspace, then the gating in place
+  if (kind == 1 || kind == 2) {
+    // a workspace smaller than the split plan's runs the launch unsplit
+    void* ws = workspace_dev && workspace_bytes >= need ? workspace_dev : nullptr;
+    g.ws = ws;
+    g.ws_bytes = ws ? workspace_bytes : 0;
+    const hipError_t e =
+        kind == 1 ? mlxr::launch_skinny_swiglu(g, u, s) : mlxr::launch_mfma_swiglu(g, u, ws, g.ws_bytes, s);
+    return e != hipSuccess ? hip_fail(e, "swiglu launch") : MLXR_OK;
+  }
+  // operands of 2 GiB or more: gate into h, up into the workspace, then the gating in place
   if (!workspace_dev || workspace_bytes < need)
     return fail(MLXR_E_INVALID, "swiglu at M=%d needs a workspace of %zu bytes (got %zu)", M, need,
                 workspace_bytes);

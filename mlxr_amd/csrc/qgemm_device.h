@@ -7,6 +7,9 @@
 
 namespace mlxr {
 
+// Cache policy bits of buffer loads (the aux operand): 0 default, 2 non-temporal (nt).
+constexpr int POL_DEFAULT = 0, POL_NT = 2;
+
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
 
@@ -183,5 +186,9 @@ __device__ __forceinline__ void dequant_raw(const RawSub<QT>& r, int j, float* w
     }
   }
 }
+
+// swish(g) * u = g / (1 + exp(-g)) * u in fp32: the gating of the SwiGLU MLP
+// (reference core/graph/layers.cpp:391-414).
+__device__ __forceinline__ float swiglu1(float g, float u) { return g / (1.f + __expf(-g)) * u; }
 
 }  // namespace mlxr

@@ -19,6 +19,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "qgemm_device.h"
 #include "qgemm_internal.h"
@@ -405,9 +406,6 @@ __global__ __launch_bounds__(256) void qgemv_kernel(GemvParams p) {
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr uint32_t OOB = 0x80000000u;  // voffset that is out of range of every buffer
 
-// swish(g) * u = g / (1 + exp(-g)) * u in fp32 (the MLP gating, layers.cpp:391-414).
-__device__ __forceinline__ float swiglu1(float g, float u) { return g / (1.f + __expf(-g)) * u; }
-
 __device__ __forceinline__ rsrc_t make_rsrc(const void* ptr, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(ptr), (short)0, (int)bytes, 0x00020000);
 }
@@ -475,38 +473,38 @@ struct LdsParams {
   LdsGroup g[MAX_GROUPS];
 };
 
-template <int QT>
+template <int QT, int WPOL>
 __device__ __forceinline__ void load_chunk(const rsrc_t* R, int row, int seg, int nsub, int nsb,
                                            int lane, bool ok, CLoad<QT>& b) {
   const uint32_t sbase = (uint32_t)row * (uint32_t)nsub + (uint32_t)seg * 64u;  // first sub-block
   const uint32_t gbase = (uint32_t)row * (uint32_t)nsb + (uint32_t)seg * 8u;    // first super-block
   if constexpr (QT == QT_Q4_K) {
-    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, WPOL);
     b.q = make_uint4(q[0], q[1], q[2], q[3]);
-    b.h = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, gbase * 16u, 0);
+    b.h = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, gbase * 16u, WPOL);
   } else if constexpr (QT == QT_Q6_K) {
-    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, WPOL);
     b.ql = make_uint4(q[0], q[1], q[2], q[3]);
-    const u32x2_t h = __builtin_amdgcn_raw_buffer_load_b64(R[1], ok ? lane * 8 : OOB, sbase * 8u, 0);
+    const u32x2_t h = __builtin_amdgcn_raw_buffer_load_b64(R[1], ok ? lane * 8 : OOB, sbase * 8u, WPOL);
     b.qh = make_uint2(h[0], h[1]);
-    b.sc = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, 0);
-    b.d = __builtin_amdgcn_raw_buffer_load_b16(R[3], ok ? (lane >> 3) * 2 : OOB, gbase * 2u, 0);
+    b.sc = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, WPOL);
+    b.d = __builtin_amdgcn_raw_buffer_load_b16(R[3], ok ? (lane >> 3) * 2 : OOB, gbase * 2u, WPOL);
   } else if constexpr (QT == QT_Q5_K) {
-    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, WPOL);
     b.q = make_uint4(q[0], q[1], q[2], q[3]);
-    b.qh = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? lane * 4 : OOB, sbase * 4u, 0);
-    b.h = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, 0);
+    b.qh = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? lane * 4 : OOB, sbase * 4u, WPOL);
+    b.h = __builtin_amdgcn_raw_buffer_load_b16(R[2], ok ? lane * 2 : OOB, gbase * 16u, WPOL);
   } else if constexpr (QT == QT_Q4_0 || QT == QT_Q4_1) {
-    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, 0);
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 16 : OOB, sbase * 16u, WPOL);
     b.q = make_uint4(q[0], q[1], q[2], q[3]);
-    if constexpr (QT == QT_Q4_0) b.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, sbase * 2u, 0);
-    else b.d = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? lane * 4 : OOB, sbase * 4u, 0);
+    if constexpr (QT == QT_Q4_0) b.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, sbase * 2u, WPOL);
+    else b.d = __builtin_amdgcn_raw_buffer_load_b32(R[1], ok ? lane * 4 : OOB, sbase * 4u, WPOL);
   } else {
-    const u32x4_t q0 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 : OOB, sbase * 32u, 0);
-    const u32x4_t q1 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 + 16 : OOB, sbase * 32u, 0);
+    const u32x4_t q0 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 : OOB, sbase * 32u, WPOL);
+    const u32x4_t q1 = __builtin_amdgcn_raw_buffer_load_b128(R[0], ok ? lane * 32 + 16 : OOB, sbase * 32u, WPOL);
     b.a = make_uint4(q0[0], q0[1], q0[2], q0[3]);
     b.b = make_uint4(q1[0], q1[1], q1[2], q1[3]);
-    b.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, sbase * 2u, 0);
+    b.d = __builtin_amdgcn_raw_buffer_load_b16(R[1], ok ? lane * 2 : OOB, sbase * 2u, WPOL);
   }
 }
 
@@ -558,7 +556,7 @@ __device__ __forceinline__ void decode_chunk(const CLoad<QT>& b, int j, uint32_t
 // SW (SwiGLU): the launch has two weights of the same shape, gate (group 0) and up (group
 // 1); a wavefront walks its gate rows, then the same up rows, and stores swish(gate) * up
 // for those rows into group 0's output.
-template <int QT, int XT, int MT, int D, bool LIN, bool SW>
+template <int QT, int XT, int MT, int D, bool LIN, bool SW, bool NT>
 __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
@@ -643,18 +641,18 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) Rs[i] = up ? RU[i] : R[i];
       if constexpr (LIN) {
-        load_chunk<QT>(Rs, r0, cc, nsub, nsb, lane, true, b);
+        load_chunk<QT, NT ? POL_NT : POL_DEFAULT>(Rs, r0, cc, nsub, nsb, lane, true, b);
       } else {
         const int rl = cc / nseg, seg = cc - rl * nseg;
-        load_chunk<QT>(Rs, min(r0 + rl, N - 1), seg, nsub, nsb, lane, seg * 64 + lane < nsub, b);
+        load_chunk<QT, NT ? POL_NT : POL_DEFAULT>(Rs, min(r0 + rl, N - 1), seg, nsub, nsb, lane, seg * 64 + lane < nsub, b);
       }
     } else if constexpr (LIN) {
       // every row is exactly nseg full segments: chunk cc starts at sub-block r0*nsub + 64*cc
-      load_chunk<QT>(R, r0, cc, nsub, nsb, lane, true, b);
+      load_chunk<QT, NT ? POL_NT : POL_DEFAULT>(R, r0, cc, nsub, nsb, lane, true, b);
     } else {
       const int rl = cc / nseg, seg = cc - rl * nseg;
       const int row = min(r0 + rl, N - 1);
-      load_chunk<QT>(R, row, seg, nsub, nsb, lane, seg * 64 + lane < nsub, b);
+      load_chunk<QT, NT ? POL_NT : POL_DEFAULT>(R, row, seg, nsub, nsb, lane, seg * 64 + lane < nsub, b);
     }
   };
 #pragma unroll
@@ -775,6 +773,10 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
 
 size_t lds_bytes(int MT, int K) { return (size_t)MT * (size_t)(((K >> 5) + 63) >> 6) * 64 * 72; }
 
+// gfx950 gives a workgroup up to 160 KiB of LDS (above 64 KiB once the kernel's limit
+// is raised).
+constexpr size_t kMaxLds = 160 * 1024;
+
 int num_cus() {
   static int cus = 0;
   if (cus == 0) {
@@ -791,29 +793,48 @@ int num_cus() {
 // Wavefronts per CU the row split aims for.  Every workgroup stages all of X in LDS, so
 // for long rows (K >= 8192: down-projection shapes) fewer, longer-lived wavefronts win:
 // the X staging traffic halves (measured on MI355X: Llama-3-8B down 10.6 -> 9.9 us at
-// M = 1).  MLXR_GEMV_WAVES_PER_CU overrides.
-int waves_per_cu_target(int K) {
-  static const int forced = getenv("MLXR_GEMV_WAVES_PER_CU") ? atoi(getenv("MLXR_GEMV_WAVES_PER_CU")) : 0;
-  if (forced > 0) return forced;
-  return K >= 8192 ? 8 : 16;
+// M = 1).
+int waves_per_cu_target(int K) { return K >= 8192 ? 8 : 16; }
+
+// Weight loads of a launch streaming at least this many bytes are non-temporal: measured
+// on MI355X (Llama-3-8B, M = 1) gate_up 15.1 -> 14.1 us and down 9.9 -> 9.6 us, while
+// the small launches (o, k/v, 2-9 MB) lose 2-5% with them.
+constexpr size_t kNtMinBytes = (size_t)16 << 20;
+
+// Raises the kernel's dynamic LDS limit on the current device (once per device).
+template <typename KernelPtr>
+hipError_t allow_lds(KernelPtr k, size_t bytes, std::atomic<uint64_t>& done) {
+  if (bytes <= 65536) return hipSuccess;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+  return e;
 }
 
-int env_int(const char* name, int dflt) {
-  const char* e = getenv(name);
-  return e ? atoi(e) : dflt;
-}
-
-template <int QT, int XT, int MT, int D, bool SW = false>
-hipError_t launch_lds_t(const LdsParams& lp, unsigned grid, hipStream_t s) {
-  if (SW && ((lp.K >> 5) & 63) == 0)
-    qgemv_lds_kernel<QT, XT, MT, D, true, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
-  else if (SW)
-    qgemv_lds_kernel<QT, XT, MT, D, false, true><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
-  else if (((lp.K >> 5) & 63) == 0)
-    qgemv_lds_kernel<QT, XT, MT, D, true, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
-  else
-    qgemv_lds_kernel<QT, XT, MT, D, false, false><<<dim3(grid), dim3(256), lds_bytes(MT, lp.K), s>>>(lp);
+template <int QT, int XT, int MT, int D, bool LIN, bool SW, bool NT>
+hipError_t launch_lds_k(const LdsParams& lp, unsigned grid, hipStream_t s) {
+  static std::atomic<uint64_t> attr{0};
+  const size_t lb = lds_bytes(MT, lp.K);
+  const hipError_t e = allow_lds(qgemv_lds_kernel<QT, XT, MT, D, LIN, SW, NT>, lb, attr);
+  if (e != hipSuccess) return e;
+  qgemv_lds_kernel<QT, XT, MT, D, LIN, SW, NT><<<dim3(grid), dim3(256), lb, s>>>(lp);
   return hipGetLastError();
+}
+
+// LIN: every row is a whole number of 64-sub-block segments.  NT (M = 1 only, where
+// launches stream the most bytes per activation): non-temporal weight loads.
+template <int QT, int XT, int MT, int D, bool SW = false>
+hipError_t launch_lds_t(const LdsParams& lp, unsigned grid, bool nt, hipStream_t s) {
+  const bool lin = ((lp.K >> 5) & 63) == 0;
+  if constexpr (MT == 1) {
+    if (nt) return lin ? launch_lds_k<QT, XT, MT, D, true, SW, true>(lp, grid, s)
+                       : launch_lds_k<QT, XT, MT, D, false, SW, true>(lp, grid, s);
+  }
+  return lin ? launch_lds_k<QT, XT, MT, D, true, SW, false>(lp, grid, s)
+             : launch_lds_k<QT, XT, MT, D, false, SW, false>(lp, grid, s);
 }
 
 // Planes addressed with 32-bit buffer offsets: every plane (and x) must stay below 2 GiB.
@@ -821,13 +842,14 @@ bool lds_fits(int M, int K, const PackedLayout& L, int MT) {
   for (int i = 0; i < L.nplanes; ++i)
     if (L.size[i] >= (1u << 31)) return false;
   if ((size_t)M * K * 2 >= (1u << 31)) return false;
-  return lds_bytes(MT, K) <= 65536;
+  return lds_bytes(MT, K) <= kMaxLds;
 }
 
 int mt_for(int M) { return M == 1 ? 1 : M <= 2 ? 2 : 4; }
 
-// Fills the launch parameters for `n` weights sharing x; returns the grid size.
-unsigned lds_setup(const RunArgs* const* items, int n, LdsParams& lp) {
+// Fills the launch parameters for `n` weights sharing x; returns the grid size.  *bytes:
+// the launch's weight bytes.
+unsigned lds_setup(const RunArgs* const* items, int n, LdsParams& lp, size_t* bytes) {
   const RunArgs& a0 = *items[0];
   const int MT = mt_for(a0.M);
   lp.x = a0.x;
@@ -843,6 +865,7 @@ unsigned lds_setup(const RunArgs* const* items, int n, LdsParams& lp) {
   int rpw = (int)min((total_rows + target - 1) / target, (long)(64 / MT));  // row results: one per lane
   if (rpw < 1) rpw = 1;
   int ws = 0;
+  *bytes = 0;
   for (int i = 0; i < n; ++i) {
     const RunArgs& a = *items[i];
     LdsGroup& G = lp.g[i];
@@ -856,20 +879,20 @@ unsigned lds_setup(const RunArgs* const* items, int n, LdsParams& lp) {
     G.y_dtype = a.y_dtype;
     G.bias_dtype = a.bias_dtype;
     ws += (a.L.N + rpw - 1) / rpw;
+    *bytes += a.L.total;
   }
   return (unsigned)((ws + 3) / 4);
 }
 
-
 template <int QT, int XT>
 hipError_t launch_lds(const RunArgs* const* items, int n, hipStream_t s) {
-  static const int depth = env_int("MLXR_GEMV_DEPTH", 3);
   LdsParams lp;
-  const unsigned grid = lds_setup(items, n, lp);
+  size_t bytes = 0;
+  const unsigned grid = lds_setup(items, n, lp, &bytes);
   const int M = lp.M;
-  if (M == 1) return depth >= 4 ? launch_lds_t<QT, XT, 1, 4>(lp, grid, s) : launch_lds_t<QT, XT, 1, 3>(lp, grid, s);
-  if (M == 2) return launch_lds_t<QT, XT, 2, 3>(lp, grid, s);
-  return launch_lds_t<QT, XT, 4, 3>(lp, grid, s);
+  if (M == 1) return launch_lds_t<QT, XT, 1, 3>(lp, grid, bytes >= kNtMinBytes, s);
+  if (M == 2) return launch_lds_t<QT, XT, 2, 3>(lp, grid, false, s);
+  return launch_lds_t<QT, XT, 4, 3>(lp, grid, false, s);
 }
 
 template <int QT, int XT, int MT, int R>
@@ -936,10 +959,10 @@ bool gemv_groupable(const RunArgs& a) { return a.M <= 4 && lds_fits(a.M, a.L.K, 
 
 template <int QT, int XT>
 hipError_t launch_lds_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t s) {
-  static const int depth = env_int("MLXR_GEMV_DEPTH", 3);
   const RunArgs* items[2] = {&gate, &up};
   LdsParams lp;
-  lds_setup(items, 2, lp);
+  size_t bytes = 0;
+  lds_setup(items, 2, lp, &bytes);
   // every wavefront works on gate rows (and the same up rows): group 1 owns no wavefronts;
   // as many wavefronts as a grouped launch of the two weights would have
   const long target = (long)num_cus() * waves_per_cu_target(gate.L.K);
@@ -949,10 +972,9 @@ hipError_t launch_lds_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t
   const int waves = (gate.L.N + lp.g[0].rows_per_wave - 1) / lp.g[0].rows_per_wave;
   const unsigned grid = (unsigned)((waves + 3) / 4);
   const int M = lp.M;
-  (void)depth;
-  if (M == 1) return launch_lds_t<QT, XT, 1, 3, true>(lp, grid, s);
-  if (M == 2) return launch_lds_t<QT, XT, 2, 3, true>(lp, grid, s);
-  return launch_lds_t<QT, XT, 4, 3, true>(lp, grid, s);
+  if (M == 1) return launch_lds_t<QT, XT, 1, 3, true>(lp, grid, bytes >= kNtMinBytes, s);
+  if (M == 2) return launch_lds_t<QT, XT, 2, 3, true>(lp, grid, false, s);
+  return launch_lds_t<QT, XT, 4, 3, true>(lp, grid, false, s);
 }
 
 hipError_t launch_gemv_grouped(const RunArgs* const* items, int n, hipStream_t s) {

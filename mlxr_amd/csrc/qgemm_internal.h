@@ -67,6 +67,20 @@ size_t mfma_grouped_workspace_bytes(const RunArgs* const* items, int n);
 hipError_t launch_skinny(const RunArgs& a, hipStream_t s);
 // Workspace bytes launch_skinny would use (0: no split).
 size_t skinny_workspace_bytes(int M, int N, int K, int qtype);
+// SwiGLU, h = swish(x.gate^T + bias_g) * (x.up^T + bias_u) into gate.y, with gate and up
+// of one type and shape; gate.ws / ws (may be null) holds split-K partials.
+// Narrow skinny kernel (M <= 32, skinny_swiglu_ok) and tiled kernel (any M; operands
+// below 2 GiB, mfma_groupable).
+bool skinny_swiglu_ok(int M);
+hipError_t launch_skinny_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t s);
+size_t skinny_swiglu_workspace_bytes(int M, int N, int K);
+hipError_t launch_mfma_swiglu(const RunArgs& gate, const RunArgs& up, void* ws, size_t ws_bytes, hipStream_t s);
+size_t mfma_swiglu_workspace_bytes(int M, int N, int K);
+// h[m][n] = swish(sum gate + bias_g) * (sum up + bias_u) over S partial planes whose rows
+// hold gate (columns 0 .. N-1) then up (N .. 2N-1) (qgemm_tile.hip).
+hipError_t launch_splitk_reduce_swiglu(const float* ws, size_t split_elems, int S, const void* bias_g,
+                                       const void* bias_u, int bias_dtype, void* y, int y_dtype, int M, int N,
+                                       hipStream_t s);
 // y = sum of S fp32 partial planes (split order) + bias, converted (qgemm_tile.hip).
 hipError_t launch_splitk_reduce(const float* ws, size_t split_elems, int S, const void* bias, int bias_dtype, void* y,
                                 int y_dtype, int M, int N, hipStream_t s);

@@ -57,7 +57,14 @@ struct SkinnyParams {
   int spg;          // K steps per workgroup (multiple of RING)
   float* ws;        // K splits over workgroups: fp32 partials, split s at ws + s * ws_split
   size_t ws_split;  // elements per split plane
+  int ws_ld;        // workspace row stride (N; 2N for SwiGLU: gate then up columns)
   uint32_t nib;
+  // SwiGLU (narrow kernel only): P2 is the up weight; a slab is 16 rows of both weights
+  // (row tile 0 gate, 1 up) and the result swish(gate + bias) * (up + bias2) goes to y
+  int swiglu;
+  PlanePtrs P2;
+  uint32_t psize2[4];
+  const void* bias2;
 };
 
 // Compile-time loop: fn(integral_constant<int, i>) for i = 0 .. N-1, fully expanded.
@@ -301,22 +308,26 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK16 - 1) / TK16;
   const int ksplit = blockIdx.x / p.slabs;
-  const int n0 = (blockIdx.x - ksplit * p.slabs) * 32;
+  const bool sw = p.swiglu != 0;
+  const int n0 = (blockIdx.x - ksplit * p.slabs) * (sw ? 16 : 32);
   const int r = lane & 15, j = lane >> 4;
   uint32_t row_sub[RT], row_sb[RT];
   bool rok[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    const int n = n0 + 16 * t + r;
+    const int n = n0 + (sw ? 0 : 16 * t) + r;
     rok[t] = n < N;
     row_sub[t] = rok[t] ? (uint32_t)n * (uint32_t)nsub : 0u;
     row_sb[t] = rok[t] ? (uint32_t)n * (uint32_t)nsb : 0u;
   }
   const int kg1 = min(nkt, (ksplit + 1) * p.spg);
   const int kt0 = ksplit * p.spg + wave * p.spw, kt1 = min(kg1, kt0 + p.spw);
-  rsrc_t R[4];
+  rsrc_t R[RT][4];  // row tile t's weight (SwiGLU: tile 1 reads the up weight)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, p.psize[i]);
+  for (int i = 0; i < 4; ++i) {
+    R[0][i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, p.psize[i]);
+    R[1][i] = sw ? make_rsrc(p.P2.p[i] ? p.P2.p[i] : (const uint8_t*)p.x, p.psize2[i]) : R[0][i];
+  }
   const rsrc_t RX = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
 
   // activations: lane (m, j) of block nb reads row nb*16 + m, K 32j .. 32j+31 of the step
@@ -347,10 +358,10 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
     const int sb = 4 * kt + j;
     const bool in = kt < kt1 && sb < nsub;
 #pragma unroll
-    for (int t = 0; t < RT; ++t) load_raw<QT>(R, row_sub[t], sb, in && rok[t], raw[slot][t]);
+    for (int t = 0; t < RT; ++t) load_raw<QT>(R[t], row_sub[t], sb, in && rok[t], raw[slot][t]);
     if constexpr (KQ && (slot & 1) == 0) {
 #pragma unroll
-      for (int t = 0; t < RT; ++t) load_hdr<QT>(R, row_sb[t], kt >> 1, in && rok[t], hdr[slot >> 1][t]);
+      for (int t = 0; t < RT; ++t) load_hdr<QT>(R[t], row_sb[t], kt >> 1, in && rok[t], hdr[slot >> 1][t]);
     }
   };
 
@@ -402,12 +413,48 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
   }
 
   // Accumulator tile (t, nb): lane holds Y[m][n .. n+3] for m = nb*16 + lane%16,
-  // n = n0 + 16t + 4(lane/16).
+  // n = n0 + 16t + 4(lane/16) (SwiGLU: n = n0 + 4(lane/16) of weight t).
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) red[wave][t * NB + nb][lane] = acc[t][nb];
   __syncthreads();
+  if (sw) {
+    // wavefront w finishes M-blocks w, w + nw, ...: gate and up sums of the same outputs
+    for (int nb = wave; nb < NB; nb += nw) {
+      const int m = nb * 16 + r;
+      if (m >= M) continue;
+      f32x4_t g = red[0][nb][lane], u = red[0][NB + nb][lane];
+      for (int w = 1; w < nw; ++w) {
+        g += red[w][nb][lane];
+        u += red[w][NB + nb][lane];
+      }
+      const int nn = n0 + 4 * j;
+      if (p.ws) {  // K split over workgroups: partial sums, gate then up columns
+        float* wsp = p.ws + (size_t)ksplit * p.ws_split + (size_t)m * p.ws_ld;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (nn + e < N) {
+            wsp[nn + e] = g[e];
+            wsp[N + nn + e] = u[e];
+          }
+        continue;
+      }
+      float v4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = nn + e < N;
+        const float gb = (p.bias && ok) ? load_scalar(p.bias, p.bias_dtype, nn + e) : 0.f;
+        const float ub = (p.bias2 && ok) ? load_scalar(p.bias2, p.bias_dtype, nn + e) : 0.f;
+        v4[e] = swiglu1(g[e] + gb, u[e] + ub);
+      }
+      const size_t rowbase = (size_t)m * N;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nn + e < N) store_scalar(p.y, p.y_dtype, rowbase + nn + e, v4[e]);
+    }
+    return;
+  }
   for (int u = wave; u < RT * NB; u += nw) {
     const int t = u / NB, nb = u - t * NB;
     const int m = nb * 16 + r;
@@ -508,15 +555,25 @@ bool use_skinny16(int M) {
   return M <= 32 && !off;
 }
 
+// The narrow kernel's plan: SwiGLU slabs are 16 rows of two weights, planned as 32-row
+// slabs of a problem with as many slabs.
+SkinnyPlan s16_plan(const SkinnyParams& sp, bool allow_split) {
+  const int Np = sp.swiglu ? 32 * ((sp.N + 15) / 16) : sp.N;
+  return skinny16_plan(Np, sp.K, allow_split, UNROLL16, MAXW, 8);
+}
+size_t s16_ws_bytes(const SkinnyParams& sp, const SkinnyPlan& pl) {
+  return pl.ks > 1 ? (size_t)pl.ks * (size_t)sp.M * (size_t)sp.N * (sp.swiglu ? 8u : 4u) : 0;
+}
+
 template <int QT, int XT>
 hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
-  sp.slabs = (sp.N + 31) / 32;
-  SkinnyPlan pl = skinny16_plan(sp.N, sp.K, sp.ws != nullptr, UNROLL16, MAXW, 8);
-  if (pl.ks > 1 && (size_t)pl.ks * (size_t)sp.M * (size_t)sp.N * 4u > ws_bytes)
-    pl = skinny16_plan(sp.N, sp.K, false, UNROLL16, MAXW, 8);
+  sp.slabs = sp.swiglu ? (sp.N + 15) / 16 : (sp.N + 31) / 32;
+  SkinnyPlan pl = s16_plan(sp, sp.ws != nullptr);
+  if (s16_ws_bytes(sp, pl) > ws_bytes) pl = s16_plan(sp, false);
   sp.spg = pl.spg;
   sp.spw = pl.spw;
-  sp.ws_split = (size_t)sp.M * (size_t)sp.N;
+  sp.ws_ld = sp.swiglu ? 2 * sp.N : sp.N;
+  sp.ws_split = (size_t)sp.M * (size_t)sp.ws_ld;
   float* const ws = (float*)sp.ws;
   void* const y = sp.y;
   const void* const bias = sp.bias;
@@ -526,6 +583,9 @@ hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   else qgemm_skinny16_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || pl.ks == 1) return e;
+  if (sp.swiglu)
+    return launch_splitk_reduce_swiglu(ws, sp.ws_split, pl.ks, bias, sp.bias2, sp.bias_dtype, y, sp.y_dtype, sp.M,
+                                       sp.N, s);
   return launch_splitk_reduce(ws, sp.ws_split, pl.ks, bias, sp.bias_dtype, y, sp.y_dtype, sp.M, sp.N, s);
 }
 
@@ -538,6 +598,7 @@ hipError_t launch_s(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   if (pl.ks > 1 && (size_t)pl.ks * (size_t)sp.M * (size_t)sp.N * 4u > ws_bytes) pl = skinny_plan(sp.N, sp.K, RING, false);
   sp.spg = pl.spg;
   sp.spw = pl.spw;
+  sp.ws_ld = sp.N;
   sp.ws_split = (size_t)sp.M * (size_t)sp.N;
   float* const ws = (float*)sp.ws;
   void* const y = sp.y;
@@ -567,6 +628,10 @@ hipError_t launch_skinny(const RunArgs& a, hipStream_t s) {
   sp.y_dtype = a.y_dtype;
   sp.nib = 0x0F0F0F0Fu;
   sp.ws = (float*)a.ws;
+  sp.swiglu = 0;
+  sp.P2 = sp.P;
+  for (int i = 0; i < 4; ++i) sp.psize2[i] = sp.psize[i];
+  sp.bias2 = nullptr;
   const size_t wsb = a.ws ? a.ws_bytes : 0;
   const bool f16 = a.x_dtype == DT_F16;
   switch (a.L.qtype) {
@@ -577,6 +642,56 @@ hipError_t launch_skinny(const RunArgs& a, hipStream_t s) {
     case QT_Q4_1: return f16 ? launch_s<QT_Q4_1, X_F16>(sp, wsb, s) : launch_s<QT_Q4_1, X_BF16>(sp, wsb, s);
     default: return f16 ? launch_s<QT_Q8_0, X_F16>(sp, wsb, s) : launch_s<QT_Q8_0, X_BF16>(sp, wsb, s);
   }
+}
+
+namespace {
+SkinnyParams swiglu_params(const RunArgs& gate, const RunArgs& up) {
+  SkinnyParams sp;
+  sp.P = plane_ptrs(gate.L, gate.packed);
+  sp.P2 = plane_ptrs(up.L, up.packed);
+  for (int i = 0; i < 4; ++i) {
+    sp.psize[i] = i < gate.L.nplanes ? (uint32_t)gate.L.size[i] : 0u;
+    sp.psize2[i] = i < up.L.nplanes ? (uint32_t)up.L.size[i] : 0u;
+  }
+  sp.x = gate.x;
+  sp.bias = gate.bias;
+  sp.bias2 = up.bias;
+  sp.y = gate.y;
+  sp.M = gate.M;
+  sp.N = gate.L.N;
+  sp.K = gate.L.K;
+  sp.bias_dtype = gate.bias_dtype;
+  sp.y_dtype = gate.y_dtype;
+  sp.nib = 0x0F0F0F0Fu;
+  sp.ws = (float*)gate.ws;
+  sp.swiglu = 1;
+  return sp;
+}
+}  // namespace
+
+bool skinny_swiglu_ok(int M) { return M <= 32; }
+
+hipError_t launch_skinny_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t s) {
+  const SkinnyParams sp = swiglu_params(gate, up);
+  const size_t wsb = gate.ws ? gate.ws_bytes : 0;
+  const bool f16 = gate.x_dtype == DT_F16;
+  switch (gate.L.qtype) {
+    case QT_Q4_K: return f16 ? launch_s16<QT_Q4_K, X_F16>(sp, wsb, s) : launch_s16<QT_Q4_K, X_BF16>(sp, wsb, s);
+    case QT_Q6_K: return f16 ? launch_s16<QT_Q6_K, X_F16>(sp, wsb, s) : launch_s16<QT_Q6_K, X_BF16>(sp, wsb, s);
+    case QT_Q5_K: return f16 ? launch_s16<QT_Q5_K, X_F16>(sp, wsb, s) : launch_s16<QT_Q5_K, X_BF16>(sp, wsb, s);
+    case QT_Q4_0: return f16 ? launch_s16<QT_Q4_0, X_F16>(sp, wsb, s) : launch_s16<QT_Q4_0, X_BF16>(sp, wsb, s);
+    case QT_Q4_1: return f16 ? launch_s16<QT_Q4_1, X_F16>(sp, wsb, s) : launch_s16<QT_Q4_1, X_BF16>(sp, wsb, s);
+    default: return f16 ? launch_s16<QT_Q8_0, X_F16>(sp, wsb, s) : launch_s16<QT_Q8_0, X_BF16>(sp, wsb, s);
+  }
+}
+
+size_t skinny_swiglu_workspace_bytes(int M, int N, int K) {
+  SkinnyParams sp;
+  sp.M = M;
+  sp.N = N;
+  sp.K = K;
+  sp.swiglu = 1;
+  return s16_ws_bytes(sp, s16_plan(sp, true));
 }
 
 size_t skinny_workspace_bytes(int M, int N, int K, int qtype) {

@@ -137,6 +137,26 @@ __global__ __launch_bounds__(256) void splitk_reduce_grouped_kernel(const float*
   store_scalar(rg.y[g], rg.y_dtype[g], (size_t)m * rg.N[g] + n, v);
 }
 
+// SwiGLU split-K: the partial planes hold gate (columns 0 .. N-1) and up (N .. 2N-1) side
+// by side; h[m][n] = swish(sum gate + bias_g) * (sum up + bias_u), sums in split order.
+__global__ __launch_bounds__(256) void splitk_reduce_swiglu_kernel(const float* __restrict__ ws, size_t split_elems,
+                                                                   int S, int N, size_t total, const void* bias_g,
+                                                                   const void* bias_u, int bias_dtype, void* y,
+                                                                   int y_dtype) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const size_t m = i / (size_t)N, n = i - m * (size_t)N;
+  const size_t gi = m * 2 * (size_t)N + n, ui = gi + (size_t)N;
+  float g = ws[gi], u = ws[ui];
+  for (int sp = 1; sp < S; ++sp) {
+    g += ws[(size_t)sp * split_elems + gi];
+    u += ws[(size_t)sp * split_elems + ui];
+  }
+  if (bias_g) g += load_scalar(bias_g, bias_dtype, n);
+  if (bias_u) u += load_scalar(bias_u, bias_dtype, n);
+  store_scalar(y, y_dtype, i, swiglu1(g, u));
+}
+
 hipError_t launch_chunk(const TileParams& tp, int bm, int S, int qtype, bool f16, hipStream_t s) {
   switch (qtype) {
     case QT_Q4_K: return launch_tile_q4k(tp, bm, S, f16, s);
@@ -180,6 +200,8 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   }
   if (sp.S > 1) {
     TileParams tp;
+  tp.swiglu = 0;
+    tp.swiglu = 0;
     tp.M = M;
     tp.K = K;
     tp.x = a.x;
@@ -211,6 +233,9 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   for (int mc = 0; mc < M; mc += Mc) {
     for (int nc = 0; nc < N; nc += Nc) {
       TileParams tp;
+  tp.swiglu = 0;
+      tp.swiglu = 0;
+    tp.swiglu = 0;
       tp.M = std::min(Mc, M - mc);
       tp.K = K;
       tp.x = (const uint8_t*)a.x + (size_t)mc * K * 2;
@@ -279,6 +304,7 @@ hipError_t launch_mfma_grouped(const RunArgs* const* items, int n, void* ws, siz
   SplitPlan sp = plan_split(M, nt * TN, K, ~(size_t)0);
   if (sp.S > 1 && (!ws || (size_t)sp.S * (size_t)M * (size_t)cols * 4u > ws_bytes)) sp = plan_split(M, nt * TN, K, 0);
   TileParams tp;
+  tp.swiglu = 0;
   tp.M = M;
   tp.K = K;
   tp.x = a.x;
@@ -326,6 +352,66 @@ hipError_t launch_mfma_grouped(const RunArgs* const* items, int n, void* ws, siz
   const size_t total = (size_t)M * (size_t)cols;
   splitk_reduce_grouped_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
       (const float*)ws, tp.ws_split, sp.S, cols, total, rg);
+  return hipGetLastError();
+}
+
+// SwiGLU: gate and up (same type and [N, K]) in one tiled launch, 128 columns of each per
+// tile; the split plan is that of a 2N-column problem.
+size_t mfma_swiglu_workspace_bytes(int M, int N, int K) {
+  if ((size_t)M * (size_t)K * 2u >= ((size_t)1 << 31)) return 0;
+  const SplitPlan sp = plan_split(M, 2 * ((N + TN / 2 - 1) / (TN / 2)) * (TN / 2), K, ~(size_t)0);
+  return sp.S > 1 ? (size_t)sp.S * (size_t)M * (size_t)N * 8u : 0;
+}
+
+hipError_t launch_mfma_swiglu(const RunArgs& gate, const RunArgs& up, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int M = gate.M, N = gate.L.N, K = gate.L.K;
+  const int tiles_n = (N + TN / 2 - 1) / (TN / 2);
+  SplitPlan sp = plan_split(M, 2 * tiles_n * (TN / 2), K, ~(size_t)0);
+  if (sp.S > 1 && (!ws || (size_t)sp.S * (size_t)M * (size_t)N * 8u > ws_bytes))
+    sp = plan_split(M, 2 * tiles_n * (TN / 2), K, 0);
+  const bool split = sp.S > 1;
+  TileParams tp;
+  tp.swiglu = 1;
+  tp.M = M;
+  tp.K = K;
+  tp.x = gate.x;
+  tp.nib = 0x0F0F0F0Fu;
+  tp.kps = split ? sp.kps : (K + TK - 1) / TK;
+  tp.ws = split ? (float*)ws : nullptr;
+  tp.ws_split = (size_t)M * (size_t)N * 2u;
+  tp.ws_ld = 2 * N;
+  tp.ngroups = 2;
+  tp.tiles_n = tiles_n;
+  const RunArgs* ab[2] = {&gate, &up};
+  for (int i = 0; i < MAX_TG; ++i) {
+    TileGroup& g = tp.g[i];
+    const RunArgs& b = *ab[i < 2 ? i : 0];
+    const PlanePtrs P = plane_ptrs(b.L, b.packed);
+    for (int k = 0; k < 4; ++k) {
+      g.P[k] = P.p[k];
+      g.psize[k] = k < b.L.nplanes ? (uint32_t)b.L.size[k] : 0u;
+    }
+    g.y = gate.y;
+    g.bias = split ? nullptr : b.bias;
+    g.N = N;
+    g.ldy = N;
+    g.tn0 = 0;
+    g.col0 = i == 1 ? N : 0;
+    g.bias_dtype = b.bias_dtype;
+    g.y_dtype = gate.y_dtype;
+  }
+  hipError_t e = launch_chunk(tp, sp.bm, split ? sp.S : 1, gate.L.qtype, gate.x_dtype == DT_F16, s);
+  if (e != hipSuccess || !split) return e;
+  return launch_splitk_reduce_swiglu((const float*)ws, tp.ws_split, sp.S, gate.bias, up.bias, gate.bias_dtype, gate.y,
+                                     gate.y_dtype, M, N, s);
+}
+
+hipError_t launch_splitk_reduce_swiglu(const float* ws, size_t split_elems, int S, const void* bias_g,
+                                       const void* bias_u, int bias_dtype, void* y, int y_dtype, int M, int N,
+                                       hipStream_t s) {
+  const size_t total = (size_t)M * (size_t)N;
+  splitk_reduce_swiglu_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
+      ws, split_elems, S, N, total, bias_g, bias_u, bias_dtype, y, y_dtype);
   return hipGetLastError();
 }
 

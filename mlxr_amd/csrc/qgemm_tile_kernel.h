@@ -85,6 +85,10 @@ struct TileParams {
   int ws_ld;        // workspace row stride (the launch's total N)
   uint32_t nib;     // 0x0F0F0F0F, passed at run time (keeps the byte converts)
   int ngroups;
+  // SwiGLU (gate = g[0], up = g[1], same shape): a tile is 128 columns of both weights,
+  // wavefronts 0-1 on gate and 2-3 on up, and the epilogue stores swish(gate) * up into
+  // g[0].y (with ws: the two weights' partials side by side, col0 0 and N)
+  int swiglu;
   TileGroup g[MAX_TG];
 };
 
@@ -93,9 +97,9 @@ struct TileParams {
 // and 64 four-byte banks, row r lands in bank group 8(r & 1) + (c ^ swz(r)), so swz must
 // be a bijection on the eight even and on the eight odd rows of an aligned group of 16.
 #ifndef MLXR_SWZ_LEGACY
-inline __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 #else
-inline __device__ __forceinline__ int swz(int r) { return r & 7; }
+__device__ __forceinline__ int swz(int r) { return r & 7; }
 #endif
 
 template <int XT>
@@ -139,10 +143,12 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
   // the weight this tile column belongs to (scalar search), its fields selected with
   // static kernel-argument offsets so every load is issued at once
+  const bool sw = p.swiglu != 0;
   int gi = 0;
 #pragma unroll
   for (int g = 1; g < MAX_TG; ++g)
     if (g < p.ngroups && tn >= p.g[g].tn0) gi = g;
+  if (sw) gi = wave >> 1;
   TileGroup G = p.g[0];
 #pragma unroll
   for (int g = 1; g < MAX_TG; ++g) {
@@ -162,7 +168,9 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     G.bias_dtype = sel ? H.bias_dtype : G.bias_dtype;
     G.y_dtype = sel ? H.y_dtype : G.y_dtype;
   }
-  const int m0 = tm * BM, n0 = (tn - G.tn0) * TN;
+  // n0: the tile's first column of weight G; wc: this wavefront's 64 columns within it
+  const int m0 = tm * BM, n0 = sw ? tn * (TN / 2) : (tn - G.tn0) * TN;
+  const int wc = sw ? 64 * (wave & 1) : 64 * wave;
   const int M = p.M, N = G.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK - 1) / TK;
@@ -211,13 +219,13 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     }
   };
 
-  // --- weight rows of this lane: n0 + 64*wave + (lane & 31) + 32j, sub-block half h
+  // --- weight rows of this lane: n0 + wc + (lane & 31) + 32j, sub-block half h
   const int h = lane >> 5;
   uint32_t row_sub[2], row_sb[2];
   bool rok[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int n = n0 + 64 * wave + (lane & 31) + 32 * j;
+    const int n = n0 + wc + (lane & 31) + 32 * j;
     rok[j] = n < N;
     row_sub[j] = rok[j] ? (uint32_t)n * (uint32_t)nsub : 0u;
     row_sb[j] = rok[j] ? (uint32_t)n * (uint32_t)nsb : 0u;
@@ -375,7 +383,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   constexpr int EP_LD = 68;
   float* ep = (float*)lds + wave * (32 * EP_LD);
   const int c4 = lane & 15;
-  const int ncol = n0 + 64 * wave + 4 * c4;  // first of this lane's four columns
+  const int ncol = n0 + wc + 4 * c4;  // first of this lane's four columns
   // output rows: y's, or the workspace's (split plane, this weight's column range)
   const int ld = p.ws ? p.ws_ld : G.ldy;
   const int cb = p.ws ? G.col0 : 0;
@@ -387,6 +395,56 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   }
   void* const out = p.ws ? (void*)(p.ws + (size_t)split * p.ws_split) : G.y;
   const int yt = p.ws ? DT_F32 : G.y_dtype;
+  if (sw && !p.ws) {
+    // SwiGLU: every wavefront parks its block (bias added) in its LDS area; gate
+    // wavefront w then reads its own block and up's (area w + 2) and stores
+    // swish(gate) * up to y (gate's columns).
+    const float* epu = (const float*)lds + (wave + 2) * (32 * EP_LD);
+    sfor<MI>([&](auto I_) {
+      constexpr int i = decltype(I_)::value;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cc = 32 * j + 8 * q + 4 * (lane >> 5);
+          float4 v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          if (G.bias) {
+            const int nc = n0 + wc + cc;
+            v.x += nc + 0 < N ? load_scalar(G.bias, G.bias_dtype, nc + 0) : 0.f;
+            v.y += nc + 1 < N ? load_scalar(G.bias, G.bias_dtype, nc + 1) : 0.f;
+            v.z += nc + 2 < N ? load_scalar(G.bias, G.bias_dtype, nc + 2) : 0.f;
+            v.w += nc + 3 < N ? load_scalar(G.bias, G.bias_dtype, nc + 3) : 0.f;
+          }
+          *(float4*)(ep + (lane & 31) * EP_LD + cc) = v;
+        }
+      __syncthreads();
+      if (wave < 2) {
+#pragma unroll 1
+        for (int r = 0; r < 8; ++r) {
+          const int row = 4 * r + (lane >> 4);
+          const float4 g = *(const float4*)(ep + row * EP_LD + 4 * c4);
+          const float4 u = *(const float4*)(epu + row * EP_LD + 4 * c4);
+          const int m = m0 + 32 * i + row;
+          if (m < M) {
+            const float o[4] = {swiglu1(g.x, u.x), swiglu1(g.y, u.y), swiglu1(g.z, u.z), swiglu1(g.w, u.w)};
+            const size_t at = (size_t)m * (size_t)G.ldy + (size_t)ncol;
+            if (vec_ok) {
+              if (yt == DT_F32) *(float4*)((float*)out + at) = make_float4(o[0], o[1], o[2], o[3]);
+              else if (yt == DT_BF16)
+                *(uint2*)((uint16_t*)out + at) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+              else *(uint2*)((uint16_t*)out + at) = make_uint2(pack2<X_F16>(o[0], o[1]), pack2<X_F16>(o[2], o[3]));
+            } else {
+#pragma unroll 1
+              for (int e = 0; e < 4; ++e)
+                if (ncol + e < N) store_scalar(out, yt, at + e, o[e]);
+            }
+          }
+        }
+      }
+      __syncthreads();
+    });
+    return;
+  }
   sfor<MI>([&](auto I_) {
     constexpr int i = decltype(I_)::value;
 #pragma unroll

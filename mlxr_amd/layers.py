@@ -83,7 +83,7 @@ class Linear:
 
 
 class MLP:
-    """down(swish(gate(x)) * up(x)); at M <= 4 gate, up and the gating are one launch."""
+    """down(swish(gate(x)) * up(x)); gate, up and the gating are one launch."""
 
     def __init__(self, hidden_size, intermediate_size):
         self.hidden_size, self.intermediate_size = hidden_size, intermediate_size
@@ -98,7 +98,7 @@ class MLP:
         x2 = x.reshape(-1, self.hidden_size)
         M = x2.shape[0]
         gw, uw = self.gate_proj.weight, self.up_proj.weight
-        if M <= 4 and (gw.qtype, gw.N) == (uw.qtype, uw.N):
+        if (gw.qtype, gw.N) == (uw.qtype, uw.N):
             h = qgemm.q_gemm_swiglu(x2, gw, uw, stream=stream)  # one fused launch
         else:
             g = self.gate_proj.forward(x2, stream=stream)

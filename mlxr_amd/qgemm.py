@@ -292,9 +292,11 @@ def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=Non
     return outs
 
 
-def q_gemm_swiglu(input, gate, up, out=None, out_dtype=None, stream=None):
+def q_gemm_swiglu(input, gate, up, out=None, out_dtype=None, stream=None, workspace=True):
     """h = swish(input . gate^T) * (input . up^T) for packed gate/up weights of one shape
-    (mlxr_qgemm_swiglu: a single fused launch at M <= 4)."""
+    (mlxr_qgemm_swiglu: one launch computes both projections and the gating; with
+    workspace, launches whose tiles cannot fill the device split K into a workspace and
+    add one reduce launch)."""
     torch = _torch()
     M, K = input.shape
     if (gate.qtype, gate.N, gate.K) != (up.qtype, up.N, up.K) or gate.K != K:
@@ -306,11 +308,12 @@ def q_gemm_swiglu(input, gate, up, out=None, out_dtype=None, stream=None):
     n = ctypes.c_size_t(0)
     _check(lib().mlxr_qgemm_swiglu_workspace_size(int(gate.qtype), gate.N, K, M, _dt_code(out.dtype), ctypes.byref(n)))
     ws = None
-    if n.value:
+    if n.value and workspace:
         with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
             ws = torch.empty(n.value, dtype=torch.uint8, device=input.device)
     _check(lib().mlxr_qgemm_swiglu(int(gate.qtype), gate.N, K, gate.data_ptr(), up.data_ptr(), input.data_ptr(),
                                    _dt_code(input.dtype), out.data_ptr(), _dt_code(out.dtype), M,
-                                   ws.data_ptr() if ws is not None else None, n.value, _stream_ptr(stream)))
+                                   ws.data_ptr() if ws is not None else None, n.value if ws is not None else 0,
+                                   _stream_ptr(stream)))
     return out
 

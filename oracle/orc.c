@@ -377,9 +377,14 @@ int orc_gemm_f64(int qtype, int M, int N, int K, const uint8_t* w, const float* 
         free(wd);
         return rc;
     }
-    if (w_to_bf16) {
+    /* w_to_bf16: 1 rounds the weights to bf16 (RNE), 2 to fp16 (RNE): the operands the
+       MFMA paths multiply for bf16 and fp16 activations */
+    if (w_to_bf16 == 1) {
 #pragma omp parallel for schedule(static)
         for (long long i = 0; i < (long long)N * K; i++) wd[i] = orc_bf16_to_f32(orc_f32_to_bf16(wd[i]));
+    } else if (w_to_bf16 == 2) {
+#pragma omp parallel for schedule(static)
+        for (long long i = 0; i < (long long)N * K; i++) wd[i] = orc_f16_to_f32(orc_f32_to_f16(wd[i]));
     }
 #pragma omp parallel for schedule(dynamic, 16)
     for (int n = 0; n < N; n++) {

@@ -98,14 +98,17 @@ def eval_cpu_cols(qtype, M, N, K, n0, n1, w, x_f32, bias=None):
     return y
 
 
-def gemm_f64(qtype, M, N, K, w, x_f32, bias=None, w_to_bf16=False, m0=0, m1=None):
-    """fp64-accumulated tolerance oracle over the exact dequantized weights, rows [m0, m1)."""
+def gemm_f64(qtype, M, N, K, w, x_f32, bias=None, w_to_bf16=False, m0=0, m1=None, w_to_f16=False):
+    """fp64-accumulated tolerance oracle over the exact dequantized weights, rows [m0, m1).
+
+    w_to_bf16 / w_to_f16 first round the weights to bf16 / fp16 (RNE): the operands the MFMA
+    paths multiply for bf16 / fp16 activations."""
     m1 = M if m1 is None else m1
     y = np.empty((m1 - m0, N), dtype=np.float32)
     x = np.ascontiguousarray(x_f32, dtype=np.float32)
     b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
-    rc = lib().orc_gemm_f64(int(qtype), M, N, K, _p(np.ascontiguousarray(w)), _p(x), _p(b),
-                            1 if w_to_bf16 else 0, m0, m1, _p(y))
+    wr = 2 if w_to_f16 else (1 if w_to_bf16 else 0)
+    rc = lib().orc_gemm_f64(int(qtype), M, N, K, _p(np.ascontiguousarray(w)), _p(x), _p(b), wr, m0, m1, _p(y))
     if rc:
         raise ValueError(f"orc_gemm_f64 rc={rc}")
     return y
@@ -125,3 +128,23 @@ def normwise_rel_err(y, ref):
     ref = np.asarray(ref, dtype=np.float64)
     den = np.max(np.abs(ref))
     return float(np.max(np.abs(y - ref)) / den) if den > 0 else float(np.max(np.abs(y - ref)))
+
+
+def elementwise_rel_err(y, ref, floor=1e-2):
+    """max_i |y_i - ref_i| / |ref_i| over the outputs with |ref_i| >= floor * max_j |ref_j|.
+
+    The floor keeps the metric away from the zeros of a random dot product, where a
+    relative error is ill-posed; 0.0 when no output qualifies (all-zero ref)."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    a = np.abs(ref)
+    big = a >= floor * np.max(a) if a.size else a.astype(bool)
+    if not np.any(big) or np.max(a) == 0:
+        return 0.0
+    return float(np.max(np.abs(y[big] - ref[big]) / a[big]))
+
+
+def rel_err(y, ref):
+    """The larger of the normwise and the elementwise relative errors (both must meet a
+    tolerance)."""
+    return max(normwise_rel_err(y, ref), elementwise_rel_err(y, ref))

@@ -1,9 +1,11 @@
 // C++ Linear / MLP layers (include/mlxr_linear.h) on the GPU: Linear::forward over a 3-D
 // input equals the q_gemm_dequant operator on the flattened rows bit for bit (same kernel
 // at these M), a GGUF-loaded weight gives the same result as one packed from host bytes,
-// and MLP::forward equals the chain (fused mlxr_qgemm_swiglu at M <= 4, else gate/up ->
-// mlxr_swiglu) -> down.  Built and run by
-// tests/test_layers.py (GPU); prints "OK <n>" on success.
+// MLP::forward equals the chain (fused mlxr_qgemm_swiglu, then down), the forward
+// overloads with caller-owned outputs and workspace equal the allocating ones, and a HIP
+// graph of them replays to the same bits.  With a second argument (a directory) it writes
+// the Linear output at M = 3 and the MLP output at M = 24 (bf16 bits) there, which
+// tests/test_layers.py checks against the oracle.  Prints "OK <n>" on success.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -47,8 +49,18 @@ static array act(int rows, int K, uint64_t seed) {
   return a;
 }
 
+static void dump(const char* dir, const char* name, const array& a) {
+  if (!dir) return;
+  const std::vector<uint8_t> h = to_host(a);
+  FILE* f = std::fopen((std::string(dir) + "/" + name).c_str(), "wb");
+  if (!f) throw std::runtime_error("dump");
+  std::fwrite(h.data(), 1, h.size(), f);
+  std::fclose(f);
+}
+
 int main(int argc, char** argv) {
   const char* gguf_path = argc > 1 ? argv[1] : nullptr;  // file with tensor "w" (Q4_K, dims {512, 384})
+  const char* out_dir = argc > 2 ? argv[2] : nullptr;
   const int K = 512, N = 384;
   std::vector<uint8_t> w((size_t)N * K / 256 * 144);
   mlxr_synth_gguf(MLXR_Q4_K, N, K, 77, w.data());
@@ -69,6 +81,14 @@ int main(int argc, char** argv) {
     array yo = kernels::q_gemm_dequant(x2, lin.weight(), M, N, K, QuantType::Q4_K, 0, &bias);
     hipDeviceSynchronize();
     EXPECT(to_host(y3) == to_host(yo));
+    // caller-owned output and workspace: same bits
+    array yc({M, N}, Dtype::bfloat16);
+    const size_t wsb = lin.workspace_size(M);
+    array w({(int)wsb + 1}, Dtype::uint8);
+    lin.forward(x3, yc, w.data<void>(), wsb);
+    hipDeviceSynchronize();
+    EXPECT(to_host(yc) == to_host(yo));
+    if (M == 3) dump(out_dir, "linear_m3.bin", yc);
   }
 
   if (gguf_path) {
@@ -101,22 +121,46 @@ int main(int argc, char** argv) {
   mlp.gate_proj().load_weight(wg.data(), QuantType::Q4_K);
   mlp.up_proj().load_weight(wu.data(), QuantType::Q4_K);
   mlp.down_proj().load_weight(wd.data(), QuantType::Q4_K);
-  for (int M : {2, 24}) {
+  for (int M : {2, 24, 100}) {
     array x = act(M, H, 50 + M);
     array y = mlp.forward(x);
     array h({M, I}, Dtype::bfloat16);
-    if (M <= 4) {
-      EXPECT(mlxr_qgemm_swiglu(MLXR_Q4_K, I, H, mlp.gate_proj().weight().data<void>(),
-                               mlp.up_proj().weight().data<void>(), x.data<void>(), MLXR_BF16, h.data<void>(),
-                               MLXR_BF16, M, nullptr, 0, nullptr) == 0);
-    } else {
-      array g = mlp.gate_proj().forward(x), u = mlp.up_proj().forward(x);
-      EXPECT(mlxr_swiglu(g.data<void>(), u.data<void>(), h.data<void>(), (size_t)M * I, MLXR_BF16, nullptr) == 0);
-      hipDeviceSynchronize();
-    }
+    EXPECT(mlxr_qgemm_swiglu(MLXR_Q4_K, I, H, mlp.gate_proj().weight().data<void>(),
+                             mlp.up_proj().weight().data<void>(), x.data<void>(), MLXR_BF16, h.data<void>(),
+                             MLXR_BF16, M, nullptr, 0, nullptr) == 0);
     array y2 = mlp.down_proj().forward(h);
     hipDeviceSynchronize();
-    EXPECT(to_host(y) == to_host(y2));
+    // unsplit chain equals the layer wherever the layer's launches do not split
+    size_t need = 0;
+    EXPECT(mlxr_qgemm_swiglu_workspace_size(MLXR_Q4_K, I, H, M, MLXR_BF16, &need) == 0);
+    if (need == 0 && mlp.down_proj().workspace_size(M) == 0) EXPECT(to_host(y) == to_host(y2));
+    // caller-owned y, h and workspace (no allocation inside): same bits as the allocating
+    // forward, eagerly and from a captured graph replayed three times
+    const size_t wsb = mlp.workspace_size(M);
+    array w({(int)wsb + 1}, Dtype::uint8);
+    array yc({M, H}, Dtype::bfloat16), hc({M, I}, Dtype::bfloat16);
+    mlp.forward(x, yc, hc, w.data<void>(), wsb);
+    hipDeviceSynchronize();
+    EXPECT(to_host(yc) == to_host(y));
+    hipStream_t cs;
+    EXPECT(hipStreamCreate(&cs) == hipSuccess);
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    array yg({M, H}, Dtype::bfloat16);
+    EXPECT(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) == hipSuccess);
+    mlp.forward(x, yg, hc, w.data<void>(), wsb, kernels::Stream{cs});
+    EXPECT(hipStreamEndCapture(cs, &graph) == hipSuccess);
+    EXPECT(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess);
+    for (int rep = 0; rep < 3; ++rep) {
+      EXPECT(hipMemset(yg.data<void>(), 0, yg.nbytes()) == hipSuccess);
+      EXPECT(hipGraphLaunch(exec, cs) == hipSuccess);
+      EXPECT(hipStreamSynchronize(cs) == hipSuccess);
+      EXPECT(to_host(yg) == to_host(y));
+    }
+    hipGraphExecDestroy(exec);
+    hipGraphDestroy(graph);
+    hipStreamDestroy(cs);
+    if (M == 24) dump(out_dir, "mlp_m24.bin", yc);
   }
   std::printf("OK %d\n", checks);
   return 0;

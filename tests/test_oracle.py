@@ -449,6 +449,36 @@ def test_gemm_bf16_weight_rounding():
     np.testing.assert_allclose(orc.gemm_f64(Q4K, M, N, K, w, x, w_to_bf16=True), ref, rtol=1e-6, atol=1e-7)
 
 
+def test_gemm_f16_weight_rounding():
+    """w_to_f16 rounds the exact weights to fp16 (RNE), the operand of the fp16 MFMA path:
+    numpy's float16 cast of the dequantized weights, then fp64."""
+    M, N, K = 2, 8, 512
+    for qt, seed in ((Q4K, 33), (Q80, 35)):
+        w = mx.synth_gguf(qt, N, K, seed)
+        x = orc.f16_bits_to_f32(mx.synth_act(M * K, mx.F16, 39)).reshape(M, K)
+        wh = orc.dequant(qt, N, K, w).astype(np.float16).astype(np.float64)
+        ref = (x.astype(np.float64) @ wh.T).astype(np.float32)
+        np.testing.assert_allclose(orc.gemm_f64(qt, M, N, K, w, x, w_to_f16=True), ref, rtol=1e-6, atol=1e-7)
+        # and it is not the bf16 rounding
+        assert not np.array_equal(orc.gemm_f64(qt, M, N, K, w, x, w_to_f16=True),
+                                  orc.gemm_f64(qt, M, N, K, w, x, w_to_bf16=True))
+
+
+def test_elementwise_rel_err_known_answers():
+    ref = np.array([100.0, -50.0, 0.5, 0.0, 1e-3])
+    # 0.5, 0.0 and 1e-3 are below 1e-2 * 100 and do not count, however wrong
+    y = np.array([101.0, -50.0, 9.0, 7.0, 5.0])
+    assert orc.elementwise_rel_err(y, ref) == pytest.approx(0.01)
+    y = np.array([100.0, -49.0, 0.5, 0.0, 1e-3])
+    assert orc.elementwise_rel_err(y, ref) == pytest.approx(0.02)
+    assert orc.elementwise_rel_err(ref, ref) == 0.0
+    assert orc.elementwise_rel_err(np.ones(3), np.zeros(3)) == 0.0
+    # the floor is relative to the largest |ref|: 2 qualifies at floor 1e-2 of 100
+    assert orc.elementwise_rel_err(np.array([100.0, 3.0]), np.array([100.0, 2.0])) == pytest.approx(0.5)
+    assert orc.rel_err(np.array([100.0, 3.0]), np.array([100.0, 2.0])) == pytest.approx(0.5)
+    assert orc.rel_err(np.array([101.0, 2.0]), np.array([100.0, 2.0])) == pytest.approx(0.01)
+
+
 def test_gemm_linearity():
     M, N, K = 3, 16, 512
     w = mx.synth_gguf(Q6K, N, K, 41)
