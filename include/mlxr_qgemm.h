@@ -141,6 +141,23 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
                       void* y_dev, int y_dtype, int M, int path, void* workspace_dev,
                       size_t workspace_bytes, void* stream);
 
+/* Bytes of the split-K scratch array mlxr_qgemm_run_noalloc keeps on each GPU. */
+#define MLXR_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* mlxr_qgemm_run_ws without a workspace argument and without any allocation: split-K
+ * partials go to a fixed device array of MLXR_NOALLOC_SCRATCH_BYTES per GPU that the
+ * library holds until the process ends.  Same arguments, kernels and results as
+ * mlxr_qgemm_run_ws with a workspace of that size.  Calls whose plan needs more scratch
+ * (mlxr_qgemm_workspace_size above MLXR_NOALLOC_SCRATCH_BYTES) fail with MLXR_E_INVALID.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU (concurrent
+ * streams or threads) race on it; serialize them.  The array keeps the last call's
+ * partials (every element a call reads it has written first).
+ * No counterpart in the reference: it exists for callers that cannot allocate device
+ * memory (HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int mlxr_qgemm_run_noalloc(int qtype, int N, int K, int group_size, const void* packed_dev,
+                           const void* x_dev, int x_dtype, const void* bias_dev, int bias_dtype,
+                           void* y_dev, int y_dtype, int M, int path, void* stream);
+
 /* One weight of a grouped call (see mlxr_qgemm_run_grouped). */
 typedef struct mlxr_qgemm_item {
   int qtype, N, K, group_size; /* as in mlxr_qgemm_run */
