@@ -18,7 +18,8 @@ launch overhead is not in their figures.)
   c4  Q4_K prefill GEMM, Llama-3-8B set, M in {512, 2048} (bf16 MFMA)
   c5  Llama-3-70B layer, Q4_K + Q6_K (v, down), 7 GEMMs in a hipGraph at M=1 and M=256,
       grouped as a decoder layer issues them (5 launches, plus split-K reduces at M=256)
-  mlp (extra) Llama-3-8B gate/up + SwiGLU gating at M=1, fused vs grouped + gating kernel
+  mlp (extra) Llama-3-8B gate/up + SwiGLU gating at M = 1, 8, 512, 2048: fused launch vs
+      grouped projections + gating kernel
   lmhead (extra) Llama-3-8B output head as Q6_K GEMV at M=1 (N = 128256)
 The CPU baseline is the reference's CPU path (dequantize all of W to fp32, then the naive
 fp32 loop; restated in oracle/orc.c) on the headline workload, one thread.
@@ -133,7 +134,68 @@ def gemm_bytes(mx, qt, M, N, K, xsz=2, ysz=2):
     return mx.gguf_size(qt, N, K) + M * K * xsz + M * N * ysz
 
 
+def rel_errs(cx, pw, x, y, bf16_w, cols=None, rows=None):
+    """Normwise max|y - ref| / max|ref| and elementwise max |y - ref| / |ref| over
+    |ref| >= 1e-2 max|ref|, with ref = fp64 x . W^T on the GPU from the library's fp32
+    dequant of the packed weight (bit-exact to the GGUF formulas, checked in the tests),
+    rounded to bf16 first for the MFMA paths, which multiply bf16 weights.  cols / rows:
+    slices of N and M (default all)."""
+    torch = cx.torch
+    W = cx.mx.dequantize(pw, torch.float32)
+    if cols is not None:
+        W = W[cols]
+    if bf16_w:
+        W = W.to(torch.bfloat16).float()
+    xs = x if rows is None else x[rows]
+    ys = y if rows is None else y[rows]
+    if cols is not None:
+        ys = ys[:, cols]
+    ref = xs.double() @ W.double().t()
+    d = (ys.double() - ref).abs()
+    a = ref.abs()
+    amax = a.max()
+    big = a >= 1e-2 * amax
+    norm = float(d.max() / amax) if amax > 0 else float(d.max())
+    elem = float((d[big] / a[big]).max()) if amax > 0 and bool(big.any()) else 0.0
+    del W
+    return {"normwise": float(f"{norm:.3e}"), "elementwise": float(f"{elem:.3e}")}
+
+
+def worst(errs):
+    """The largest normwise and elementwise errors over a list of rel_errs results."""
+    return {"normwise": max(e["normwise"] for e in errs), "elementwise": max(e["elementwise"] for e in errs)}
+
+
 # ------------------------------------------------------------------------------ headline
+
+def stream_read_step_ms(cx, args, step_launches):
+    """Graph-replayed time of a step whose launches only stream-read the given packed
+    weights: step_launches = [[[PackedWeight, ...] per launch] per layer]."""
+    import ctypes
+    mx, torch = cx.mx, cx.torch
+    sink = torch.zeros(1024, dtype=torch.int32, device=cx.dev)
+    calls = []
+    for layer in step_launches:
+        for pws in layer:
+            ptrs = (ctypes.c_void_p * len(pws))(*[pw.data_ptr() for pw in pws])
+            sizes = (ctypes.c_size_t * len(pws))(*[pw.nbytes for pw in pws])
+            grid = int(min(-(-sum(pw.nbytes for pw in pws) // (16 * 1024)), 2048))
+            calls.append((len(pws), ptrs, sizes, grid))
+    lib = mx.qgemm.lib()
+
+    def step():
+        st = mx.qgemm._stream_ptr(None)
+        for n, ptrs, sizes, grid in calls:
+            mx.qgemm._check(lib.mlxr_bench_stream_read(n, ptrs, sizes, sink.data_ptr(), grid, st))
+
+    g = cx.graph(step)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = cx.event_ms(lambda r: g.replay(), args.steps)
+    del g
+    return ms
+
 
 def cpu_model():
     """The host CPU's model name (/proc/cpuinfo), for the CPU baselines."""
@@ -206,6 +268,10 @@ def run_headline(cx, args, out):
     torch.cuda.synchronize()
     ms_model = cx.event_ms(lambda r: model.replay(), args.steps)
     del model
+    # the same step's launch structure with a pure streaming read of the same packed weight
+    # buffers in place of each GEMV launch (mlxr_bench_stream_read): the HBM ceiling of
+    # 4 launches per layer, 128 per step, in one graph
+    ms_ceiling = stream_read_step_ms(cx, args, [[[W[n] for n in names] for _, names in LAUNCHES] for W in copies])
     # one layer per graph (a graph launch per 4 kernels), for comparison
     graphs = [cx.graph(lambda W=W: step(W)) for W in copies[:8]]
     for c in range(args.warmup):
@@ -234,6 +300,11 @@ def run_headline(cx, args, out):
         dst.copy_(src)
         torch.cuda.synchronize()
 
+    # accuracy of one layer of the step (as the graph ran it): every output
+    step(copies[0])
+    torch.cuda.synchronize()
+    head_err = worst([rel_errs(cx, copies[0][n], x[dims[n][1]], ys[n], False) for n, _, _ in LLAMA3_8B])
+
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         for line in open(TRAFFIC_FILE):
@@ -248,8 +319,16 @@ def run_headline(cx, args, out):
                      "kernel": "qgemv_lds_kernel<Q4_K,bf16,M=1> (4 launches per step: qkv, o, gate_up, down)",
                      "kernel_avg_us": round(avg_us, 3), "alg_bytes_per_launch": round(step_bytes / len(LAUNCHES))},
         "headline_detail": {
+            "max_rel_err": head_err,
             "layers_per_step": len(copies), "layer_bytes": step_bytes,
             "us_per_layer": round(1e3 * ms_model / len(copies), 3),
+            "stream_read_ceiling": {
+                "what": "pure non-temporal streaming read of the same packed weight buffers in the same "
+                        "launch structure (4 launches per layer, 128 per step, one graph), nothing computed",
+                "ms_per_step": round(ms_ceiling, 5),
+                "GBps": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9, 1),
+                "frac_hbm": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "gemv_step_vs_ceiling": round(ms_ceiling / ms_model, 4)},
             "one_layer_graph_ms": round(ms_graph, 5),
             "one_layer_graph_GBps": round(step_bytes / (ms_graph * 1e-3) / 1e9, 1),
             "launches": {ln: {"us": round(kern_us[ln], 3), "bytes": lbytes[ln],
@@ -330,8 +409,10 @@ def run_c1(cx, args):
         fn(r)
     us = 1e3 * cx.graph_ms(fn, len(copies))
     b = gemm_bytes(mx, Q80, 1, N, K)
+    fn(0)
+    err = rel_errs(cx, copies[0]["q"], x, y, False)
     return {"shape": "M=1 K=2048 N=2048 Q8_0, x/y fp16", "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
-            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": b}
+            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "alg_bytes": b, "max_rel_err": err}
 
 
 def run_c3(cx, args):
@@ -349,8 +430,10 @@ def run_c3(cx, args):
                 fn = lambda r: mx.q_gemm_dequant(x[K], copies[r % len(copies)][n], M, N, K, Q4K, out=y, path=path)
                 fn(0)
                 us = 1e3 * cx.graph_ms(fn, 2 * len(copies))
+                fn(0)
+                err = rel_errs(cx, copies[0][n], x[K], y, path == mx.PATH_MFMA)
                 row[f"{n}_{pname}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1),
-                                       "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                       "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "max_rel_err": err}
         res[f"M={M}"] = row
     return res
 
@@ -371,7 +454,10 @@ def run_c4(cx, args):
             fn(0)
             us = 1e3 * cx.graph_ms(fn, 5 if M == 2048 else 10)
             f = 2.0 * M * N * K
-            shapes[n] = {"us": round(us, 1), "TFLOPs": round(f / us / 1e6, 1)}
+            fn(0)
+            # every column, rows in three 64-row slices (first, middle, last)
+            errs = [rel_errs(cx, W[n], x[K], y, True, rows=slice(m0, m0 + 64)) for m0 in (0, M // 2, M - 64)]
+            shapes[n] = {"us": round(us, 1), "TFLOPs": round(f / us / 1e6, 1), "max_rel_err": worst(errs)}
             tot_f += f
             tot_us += us
         # the same seven GEMMs as a decoder layer issues them: q/k/v and gate/up as grouped
@@ -407,28 +493,57 @@ def run_c4(cx, args):
 
 
 def run_mlp(cx, args):
-    """Llama-3-8B MLP gate/up half at M = 1: fused gate + up + gating (one launch) against the
-    grouped gate/up launch followed by the gating kernel.  Not a BASELINE config."""
+    """Llama-3-8B MLP gate/up half (K = 4096, N = 14336) at M = 1, 8, 512 and 2048: the fused
+    gate + up + gating launch (mlxr_qgemm_swiglu; GEMV, narrow skinny and tiled kernels)
+    against the grouped gate/up projections followed by the gating kernel.  Not a BASELINE
+    config (the reference plans the fusion in swiglu_mlp_fused.metal:131-345)."""
     mx, torch = cx.mx, cx.torch
     specs = [(n, N, K, Q4K) for n, N, K in LLAMA3_8B if n in ("gate", "up")]
     _, copies, _ = pack_copies(cx, specs, SEED_BASE + 6)
-    x = cx.act(1, 4096, mx.BF16, SEED_BASE + 6001)
-    h = torch.empty((1, 14336), dtype=torch.bfloat16, device=cx.dev)
-    g = torch.empty_like(h)
-    u = torch.empty_like(h)
-    fused = lambda r: mx.q_gemm_swiglu(x, copies[r % len(copies)]["gate"], copies[r % len(copies)]["up"], out=h)
-
-    def unfused(r):
-        W = copies[r % len(copies)]
-        mx.q_gemm_dequant_grouped(x, [W["gate"], W["up"]], outs=[g, u])
-        mx.swiglu(g, u, out=h)
-
-    b = 2 * mx.gguf_size(Q4K, 14336, 4096) + 4096 * 2 + 14336 * 2
+    N, K = 14336, 4096
     res = {}
-    for name, fn in (("fused", fused), ("grouped_plus_gating", unfused)):
-        fn(0)
-        us = 1e3 * cx.graph_ms(fn, 2 * len(copies))
-        res[name] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+    for M in (1, 8, 512, 2048):
+        x = cx.act(M, K, mx.BF16, SEED_BASE + 6001 + M)
+        h = torch.empty((M, N), dtype=torch.bfloat16, device=cx.dev)
+        g = torch.empty_like(h)
+        u = torch.empty_like(h)
+        fused = lambda r: mx.q_gemm_swiglu(x, copies[r % len(copies)]["gate"], copies[r % len(copies)]["up"], out=h)
+
+        def unfused(r):
+            W = copies[r % len(copies)]
+            mx.q_gemm_dequant_grouped(x, [W["gate"], W["up"]], outs=[g, u])
+            mx.swiglu(g, u, out=h)
+
+        b = 2 * mx.gguf_size(Q4K, N, K) + M * K * 2 + M * N * 2
+        f = 2.0 * 2 * M * N * K
+        row = {}
+        for name, fn in (("fused", fused), ("grouped_plus_gating", unfused)):
+            fn(0)
+            us = 1e3 * cx.graph_ms(fn, 2 * len(copies) if M <= 8 else 4)
+            row[name] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1), "TFLOPs": round(f / us / 1e6, 1)}
+        # accuracy of the fused launch: fp64 gating of fp64 gate/up (bf16 weights where the
+        # MFMA kernels run), 256 columns at both ends
+        fused(0)
+        torch.cuda.synchronize()
+        errs = []
+        for cols in (slice(0, 256), slice(N - 256, N)):
+            rows = None if M <= 64 else slice(0, 64)
+            ref = []
+            for nm in ("gate", "up"):
+                W = mx.dequantize(copies[0][nm], torch.float32)[cols]
+                if M > 4:
+                    W = W.to(torch.bfloat16).float()
+                xs = x if rows is None else x[rows]
+                ref.append(xs.double() @ W.double().t())
+            r = ref[0] / (1.0 + torch.exp(-ref[0])) * ref[1]
+            hs = (h if rows is None else h[rows])[:, cols].double()
+            d, a = (hs - r).abs(), r.abs()
+            big = a >= 1e-2 * a.max()
+            errs.append({"normwise": float(f"{float(d.max() / a.max()):.3e}"),
+                         "elementwise": float(f"{float((d[big] / a[big]).max()):.3e}")})
+        row["fused_max_rel_err"] = worst(errs)
+        row["fused_speedup"] = round(row["grouped_plus_gating"]["us"] / row["fused"]["us"], 3)
+        res[f"M={M}"] = row
     return res
 
 
@@ -469,13 +584,18 @@ def run_c5(cx, args):
             graphs[r % len(graphs)].replay()
         torch.cuda.synchronize()
         ms = cx.event_ms(lambda r: graphs[r % len(graphs)].replay(), 10 if M == 1 else 4)
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        rows = None if M == 1 else slice(0, 64)
+        err = worst([rel_errs(cx, copies[0][n], x[K], ys[n], M > 4, rows=rows) for n, _, K, _ in LLAMA3_70B])
         byts = sum(gemm_bytes(mx, qt, M, N, K) for _, N, K, qt in LLAMA3_70B)
         flops = sum(2.0 * M * N * K for _, N, K, qt in LLAMA3_70B)
         res[f"M={M}"] = {"ms_per_layer": round(ms, 4), "launches_per_layer": 5,
                          "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
                          "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
-                         "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+                         "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                         "max_rel_err": err}
         del graphs
         if M > 4:
             # beside it: the seven projections as seven separate calls
@@ -519,7 +639,7 @@ def main():
         run_headline(cx, args, out)
     configs = {}
     for key, fn in (("c1_q8_0_gemv_tinyllama", run_c1), ("c3_q4k_skinny", run_c3), ("c4_q4k_prefill", run_c4),
-                    ("c5_llama3_70b_layer_graph", run_c5), ("mlp_swiglu_m1", run_mlp),
+                    ("c5_llama3_70b_layer_graph", run_c5), ("mlp_swiglu", run_mlp),
                     ("lmhead_q6k_llama3_8b_m1", run_lmhead)):
         if key.split("_")[0] in only:
             configs[key] = fn(cx, args)

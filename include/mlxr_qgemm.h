@@ -209,6 +209,14 @@ int mlxr_qgemm_swiglu(int qtype, int N, int K, const void* gate_packed, const vo
  * core/graph/layers.cpp:391-414, MLP::forward). */
 int mlxr_swiglu(const void* gate_dev, const void* up_dev, void* out_dev, size_t n, int dtype, void* stream);
 
+/* Benchmark probe, not part of the matmul path: one launch of `grid` workgroups that only
+ * reads bytes[i] bytes (multiples of 16) of each of the nbuf (1-4) device buffers bufs[i],
+ * with non-temporal loads, and writes nothing (sink_dev: 4 KiB of device memory it could
+ * write).  bench.py times it over the headline step's weights in the step's launch
+ * structure, as the HBM ceiling of that structure.  No counterpart in the reference. */
+int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const size_t* bytes, void* sink_dev, int grid,
+                           void* stream);
+
 /* Deterministic synthetic inputs with the shapes/distributions of the benchmark
  * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by
  * Box-Muller in double precision.

@@ -18,7 +18,7 @@ ARCH = "gfx950"
 # longest compiles first (the pool starts them first)
 SOURCES = ["qgemm_gemv.hip", "qgemm_tile_q4k.hip", "qgemm_tile_q6k.hip", "qgemm_tile_q5k.hip",
            "qgemm_tile_q40.hip", "qgemm_tile_q41.hip", "qgemm_tile_q80.hip", "qgemm_skinny.hip",
-           "qgemm_tile.hip", "qgemm_api.hip", "qgemm_pack.hip", "qgemm_noalloc.hip",
+           "qgemm_tile.hip", "qgemm_api.hip", "qgemm_pack.hip", "qgemm_noalloc.hip", "probe.hip",
            "q_gemm_dequant_primitive.cpp", "synth.cpp", "gguf.cpp", "act.hip", "linear.cpp"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-Wall",
           # packed fp32 VALU ops are kept out of the device code

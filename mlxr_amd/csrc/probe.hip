@@ -1,0 +1,76 @@
+// Measurement kernel for the benchmark (not part of the matmul path): a pure streaming
+// read of up to four device buffers in one launch, the bytes a grouped GEMV launch reads,
+// with nothing computed on them.  bench.py runs it over the headline step's packed weights
+// in the step's launch structure (one launch per grouped projection, one graph) to give
+// the HBM ceiling that structure allows.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mlxr_qgemm.h"
+#include "qgemm_device.h"
+#include "qgemm_internal.h"
+
+namespace mlxr {
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+
+struct ReadParams {
+  const uint8_t* p[4];
+  size_t n16[4];   // 16-byte units of each buffer
+  size_t start[4];  // first unit of buffer i in the launch's concatenated range
+  size_t total;
+  int nbuf;
+  uint32_t* sink;
+};
+
+// Threads take 16-byte units of the concatenated range in a grid-stride loop, four loads
+// in flight each; the XOR of the data goes to sink only if it equals a value no input
+// here produces, so the loads cannot be dropped and nothing is written.
+__global__ __launch_bounds__(256) void stream_read_kernel(ReadParams rp) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  uint32_t acc = 0;
+  for (size_t base = (size_t)blockIdx.x * 256 + threadIdx.x; base < rp.total; base += 4 * stride) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const size_t i = base + u * stride;
+      v[u] = u32x4_t{0, 0, 0, 0};
+      if (i < rp.total) {
+        int b = 0;
+#pragma unroll
+        for (int k = 1; k < 4; ++k)
+          if (k < rp.nbuf && i >= rp.start[k]) b = k;
+        const u32x4_t* q = (const u32x4_t*)rp.p[b] + (i - rp.start[b]);
+        v[u] = __builtin_nontemporal_load(q);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  if (acc == 0x9E3779B9u && threadIdx.x == 0) rp.sink[blockIdx.x & 1023] = acc;
+}
+
+}  // namespace
+}  // namespace mlxr
+
+extern "C" int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const size_t* bytes, void* sink_dev,
+                                      int grid, void* stream) {
+  if (nbuf < 1 || nbuf > 4 || !bufs || !bytes || !sink_dev || grid < 1)
+    return mlxr::set_error(MLXR_E_INVALID, "mlxr_bench_stream_read: 1-4 buffers, a sink and a grid");
+  mlxr::ReadParams rp;
+  rp.total = 0;
+  rp.nbuf = nbuf;
+  rp.sink = (uint32_t*)sink_dev;
+  for (int i = 0; i < 4; ++i) {
+    const int k = i < nbuf ? i : 0;
+    if (!bufs[k] || (bytes[k] & 15)) return mlxr::set_error(MLXR_E_INVALID, "buffers must be 16-byte multiples");
+    rp.p[i] = (const uint8_t*)bufs[k];
+    rp.n16[i] = i < nbuf ? bytes[k] / 16 : 0;
+    rp.start[i] = rp.total;
+    rp.total += rp.n16[i];
+  }
+  mlxr::stream_read_kernel<<<dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream>>>(rp);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MLXR_OK : mlxr::set_error(MLXR_E_HIP, "stream read launch: %s", hipGetErrorString(e));
+}

@@ -24,10 +24,7 @@ constexpr int kGemvMaxM = 4;
 // shapes: at M = 32 the skinny kernel's 16x16x32 variant is ahead, gate 26.9 vs 29.0 us
 // and down 26.7 vs 29.7 us; at M = 64 the tiled one, gate 28.3 vs 42.7 us).
 constexpr int kSkinnyOnlyMaxM = 32;
-int skinny_only_max_m() {  // MLXR_SKINNY_ONLY_MAX_M overrides (tuning)
-  static const int v = getenv("MLXR_SKINNY_ONLY_MAX_M") ? atoi(getenv("MLXR_SKINNY_ONLY_MAX_M")) : kSkinnyOnlyMaxM;
-  return v;
-}
+int skinny_only_max_m() { return kSkinnyOnlyMaxM; }
 
 thread_local std::string g_err;
 
@@ -44,6 +41,13 @@ int fail(int code, const char* fmt, ...) {
 }  // namespace
 
 namespace mlxr {
+
+size_t operand_limit() {
+  // test hook only (documented in qgemm_internal.h); read per call so a test can set it
+  const char* e = getenv("MLXR_MFMA_CHUNK_BYTES");
+  const long long v = e ? atoll(e) : 0;
+  return v > 0 ? std::min((size_t)1 << 31, (size_t)v) : (size_t)1 << 31;
+}
 
 int set_error(int code, const char* fmt, ...) {
   char buf[512];
@@ -222,7 +226,9 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   bool skinny = false;
   if (!gemv && M <= 64) {
     const size_t need = M > skinny_only_max_m() ? mlxr::mfma_workspace_bytes(M, a.L.N, a.L.K) : 0;
-    skinny = need == 0 || !a.ws || a.ws_bytes < need;
+    // the skinny kernels address operands with 32-bit offsets; the tiled launcher splits
+    // larger problems into chunks
+    skinny = (need == 0 || !a.ws || a.ws_bytes < need) && mlxr::skinny_fits(a);
   }
   hipError_t e;
   if (gemv) e = mlxr::launch_gemv(a, (hipStream_t)stream);

@@ -839,9 +839,10 @@ hipError_t launch_lds_t(const LdsParams& lp, unsigned grid, bool nt, hipStream_t
 
 // Planes addressed with 32-bit buffer offsets: every plane (and x) must stay below 2 GiB.
 bool lds_fits(int M, int K, const PackedLayout& L, int MT) {
+  const size_t lim = operand_limit();
   for (int i = 0; i < L.nplanes; ++i)
-    if (L.size[i] >= (1u << 31)) return false;
-  if ((size_t)M * K * 2 >= (1u << 31)) return false;
+    if (L.size[i] >= lim) return false;
+  if ((size_t)M * K * 2 >= lim) return false;
   return lds_bytes(MT, K) <= kMaxLds;
 }
 

@@ -62,15 +62,22 @@ bool mfma_groupable(const RunArgs& a);
 hipError_t launch_mfma_grouped(const RunArgs* const* items, int n, void* ws, size_t ws_bytes, hipStream_t s);
 size_t mfma_grouped_workspace_bytes(const RunArgs* const* items, int n);
 
+// Largest operand (activations, weight plane) the 32-bit-offset kernels address in one
+// launch: 2 GiB.  Test hook: the environment variable MLXR_MFMA_CHUNK_BYTES lowers it (read
+// on each call), so the tests reach the chunked and fallback launches at small sizes.
+size_t operand_limit();
+
 // Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.  With a.ws,
 // shapes with fewer 32-row slabs than CUs also split K over workgroups.
 hipError_t launch_skinny(const RunArgs& a, hipStream_t s);
+// Whether every operand of a is below operand_limit() (else: launch_mfma, which chunks).
+bool skinny_fits(const RunArgs& a);
 // Workspace bytes launch_skinny would use (0: no split).
 size_t skinny_workspace_bytes(int M, int N, int K, int qtype);
 // SwiGLU, h = swish(x.gate^T + bias_g) * (x.up^T + bias_u) into gate.y, with gate and up
 // of one type and shape; gate.ws / ws (may be null) holds split-K partials.
 // Narrow skinny kernel (M <= 32, skinny_swiglu_ok) and tiled kernel (any M; operands
-// below 2 GiB, mfma_groupable).
+// below 2 GiB, mfma_groupable; no biases).
 bool skinny_swiglu_ok(int M);
 hipError_t launch_skinny_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t s);
 size_t skinny_swiglu_workspace_bytes(int M, int N, int K);

@@ -511,7 +511,7 @@ struct SkinnyPlan {
   int ks, spg, w, spw;
 };
 SkinnyPlan skinny_plan(int N, int K, int ring, bool allow_split) {
-  static const int wpc = getenv("MLXR_SKINNY_WPC") ? atoi(getenv("MLXR_SKINNY_WPC")) : 8;
+  constexpr int wpc = 8;  // wavefronts per CU aimed for
   const int cus = device_cus_s();
   const int slabs = (N + 31) / 32;
   const int nkt = (K + TK - 1) / TK;
@@ -550,10 +550,7 @@ SkinnyPlan skinny16_plan(int N, int K, bool allow_split, int unroll, int wcap, i
   return pl;
 }
 
-bool use_skinny16(int M) {
-  static const int off = getenv("MLXR_SKINNY16_OFF") ? atoi(getenv("MLXR_SKINNY16_OFF")) : 0;
-  return M <= 32 && !off;
-}
+bool use_skinny16(int M) { return M <= 32; }
 
 // The narrow kernel's plan: SwiGLU slabs are 16 rows of two weights, planned as 32-row
 // slabs of a problem with as many slabs.
@@ -692,6 +689,14 @@ size_t skinny_swiglu_workspace_bytes(int M, int N, int K) {
   sp.K = K;
   sp.swiglu = 1;
   return s16_ws_bytes(sp, s16_plan(sp, true));
+}
+
+bool skinny_fits(const RunArgs& a) {
+  const size_t lim = operand_limit();
+  if ((size_t)a.M * (size_t)a.L.K * 2u >= lim) return false;
+  for (int i = 0; i < a.L.nplanes; ++i)
+    if (a.L.size[i] >= lim) return false;
+  return true;
 }
 
 size_t skinny_workspace_bytes(int M, int N, int K, int qtype) {

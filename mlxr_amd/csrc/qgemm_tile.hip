@@ -41,21 +41,17 @@ struct SplitPlan {
   int bm, tiles, S, kps;
 };
 SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
-  static const int force_bm = getenv("MLXR_MFMA_BM") ? atoi(getenv("MLXR_MFMA_BM")) : 0;
-  static const int force_s = getenv("MLXR_MFMA_SPLIT") ? atoi(getenv("MLXR_MFMA_SPLIT")) : 0;
   const int nkt = (K + TK - 1) / TK, cus = device_cus();
   const long tn = (N + TN - 1) / TN;
   SplitPlan best{256, 0, 1, 0};
   double best_t = 1e30;
   for (int bm : {256, 128, 64}) {
-    if ((force_bm == 64 || force_bm == 128 || force_bm == 256) && bm != force_bm) continue;
     const long tiles = ((M + bm - 1) / bm) * tn;
     for (int S = 1; S <= 8; ++S) {
-      if (force_s >= 1 && S != std::min(force_s, (nkt + 3) / 4)) continue;
       const int kps = (((nkt + S - 1) / S) + 3) / 4 * 4;
       const int Sr = (nkt + kps - 1) / kps;  // splits actually used
       if (Sr != S) continue;
-      if (S > 1 && ((force_s < 1 && kps < 8) || (size_t)S * (size_t)M * (size_t)N * 4u > ws_bytes)) continue;
+      if (S > 1 && (kps < 8 || (size_t)S * (size_t)M * (size_t)N * 4u > ws_bytes)) continue;
       const long rounds = (tiles * S + cus - 1) / cus;
       double t = (double)rounds * (kps * (bm == 256 ? 1.0 : bm == 128 ? 0.64 : 0.5) + 0.8);
       if (S > 1) t += (3.0 + (double)S * M * N * 8.0 / 5e6) / 1.86;
@@ -65,12 +61,8 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
       }
     }
   }
-  if (best.kps == 0) {  // nothing qualified (a forced split without workspace): no split
-    best.bm = (force_bm == 64 || force_bm == 128) ? force_bm : 256;
-    best.tiles = (int)(((M + best.bm - 1) / best.bm) * tn);
-    best.S = 1;
-    best.kps = nkt;
-  }
+
+  if (best.kps == 0) best = SplitPlan{256, (int)(((M + 255) / 256) * tn), 1, nkt};  // not reached: S = 1 qualifies
   return best;
 }
 
@@ -177,9 +169,7 @@ size_t dtype_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
 // a whole number per weight row, so an N chunk is a row range of every plane).
 hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   const int M = a.M, N = a.L.N, K = a.L.K;
-  // (MLXR_MFMA_CHUNK_BYTES lowers the limit, so tests can exercise the chunked launches)
-  const char* cl = getenv("MLXR_MFMA_CHUNK_BYTES");
-  const size_t lim = cl ? std::min((size_t)1 << 31, (size_t)std::max(1LL, atoll(cl))) : (size_t)1 << 31;
+  const size_t lim = operand_limit();
   size_t prb[4] = {0, 0, 0, 0};
   size_t max_prb = 1;
   for (int i = 0; i < a.L.nplanes; ++i) {
@@ -271,9 +261,10 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
 // whose tile columns run over the weights in turn; the split plan is that of the
 // concatenated N.  Requires every operand below 2 GiB (mfma_groupable).
 bool mfma_groupable(const RunArgs& a) {
-  if ((size_t)a.M * (size_t)a.L.K * 2u >= ((size_t)1 << 31)) return false;
+  const size_t lim = operand_limit();
+  if ((size_t)a.M * (size_t)a.L.K * 2u >= lim) return false;
   for (int i = 0; i < a.L.nplanes; ++i)
-    if (a.L.size[i] >= ((size_t)1 << 31)) return false;
+    if (a.L.size[i] >= lim) return false;
   return true;
 }
 
@@ -364,6 +355,7 @@ size_t mfma_swiglu_workspace_bytes(int M, int N, int K) {
 }
 
 hipError_t launch_mfma_swiglu(const RunArgs& gate, const RunArgs& up, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (gate.bias || up.bias) return hipErrorInvalidValue;  // the tiled SwiGLU epilogue adds no bias
   const int M = gate.M, N = gate.L.N, K = gate.L.K;
   const int tiles_n = (N + TN / 2 - 1) / (TN / 2);
   SplitPlan sp = plan_split(M, 2 * tiles_n * (TN / 2), K, ~(size_t)0);
@@ -392,7 +384,7 @@ hipError_t launch_mfma_swiglu(const RunArgs& gate, const RunArgs& up, void* ws, 
       g.psize[k] = k < b.L.nplanes ? (uint32_t)b.L.size[k] : 0u;
     }
     g.y = gate.y;
-    g.bias = split ? nullptr : b.bias;
+    g.bias = nullptr;
     g.N = N;
     g.ldy = N;
     g.tn0 = 0;

@@ -85,9 +85,10 @@ struct TileParams {
   int ws_ld;        // workspace row stride (the launch's total N)
   uint32_t nib;     // 0x0F0F0F0F, passed at run time (keeps the byte converts)
   int ngroups;
-  // SwiGLU (gate = g[0], up = g[1], same shape): a tile is 128 columns of both weights,
-  // wavefronts 0-1 on gate and 2-3 on up, and the epilogue stores swish(gate) * up into
-  // g[0].y (with ws: the two weights' partials side by side, col0 0 and N)
+  // SwiGLU (gate = g[0], up = g[1], same shape): a tile is 128 output columns; wavefront
+  // w's two 32-column accumulator blocks are gate and up of the same 32 columns, and the
+  // epilogue stores swish(gate) * up into g[0].y (with ws: the two weights' partials side
+  // by side, columns n and N + n of rows of ws_ld = 2N)
   int swiglu;
   TileGroup g[MAX_TG];
 };
@@ -122,7 +123,9 @@ __device__ __forceinline__ void sfor(Fn&& fn) {
   sfor_impl(fn, std::make_integer_sequence<int, N>());
 }
 
-template <int QT, int XT, int MI>
+// SW: the SwiGLU variant (p.swiglu set; a separate instantiation, so the plain kernel's
+// code and registers are those of the kernel without it).
+template <int QT, int XT, int MI, bool SW>
 __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   constexpr int BM = 32 * MI;              // tile rows (M)
   constexpr int A_STAGE = BM * TK * 2;     // bytes per activation stage
@@ -143,12 +146,12 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
   // the weight this tile column belongs to (scalar search), its fields selected with
   // static kernel-argument offsets so every load is issued at once
-  const bool sw = p.swiglu != 0;
+  constexpr bool sw = SW;
   int gi = 0;
 #pragma unroll
   for (int g = 1; g < MAX_TG; ++g)
     if (g < p.ngroups && tn >= p.g[g].tn0) gi = g;
-  if (sw) gi = wave >> 1;
+  if constexpr (sw) gi = 0;  // gate; block 1 reads p.g[1] (up) directly
   TileGroup G = p.g[0];
 #pragma unroll
   for (int g = 1; g < MAX_TG; ++g) {
@@ -168,18 +171,24 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     G.bias_dtype = sel ? H.bias_dtype : G.bias_dtype;
     G.y_dtype = sel ? H.y_dtype : G.y_dtype;
   }
-  // n0: the tile's first column of weight G; wc: this wavefront's 64 columns within it
+  // n0: the tile's first column of weight G; wc: this wavefront's columns within it (64;
+  // SwiGLU: 32 of gate and the same 32 of up)
   const int m0 = tm * BM, n0 = sw ? tn * (TN / 2) : (tn - G.tn0) * TN;
-  const int wc = sw ? 64 * (wave & 1) : 64 * wave;
+  const int wc = sw ? 32 * wave : 64 * wave;
   const int M = p.M, N = G.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK - 1) / TK;
   // this workgroup's K steps [kt0, kend): kt0 is a multiple of four (super-block start)
   const int kt0 = split * p.kps, kend = min(nkt, kt0 + p.kps);
 
-  rsrc_t R[4];
+  // weight of accumulator block j (SwiGLU: block 1 reads the up weight)
+  rsrc_t R[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) R[i] = make_rsrc(G.P[i] ? G.P[i] : (const uint8_t*)p.x, G.psize[i]);
+  for (int i = 0; i < 4; ++i) {
+    R[0][i] = make_rsrc(G.P[i] ? G.P[i] : (const uint8_t*)p.x, G.psize[i]);
+    if constexpr (sw) R[1][i] = make_rsrc(p.g[1].P[i] ? p.g[1].P[i] : (const uint8_t*)p.x, p.g[1].psize[i]);
+    else R[1][i] = R[0][i];
+  }
 
   // --- activations: LDS DMA.  Wave w fills slot blocks MI*w .. MI*w+MI-1 of a stage
   // (1 KiB = 8 rows each); lane l of block b brings row 8b + l/8, global chunk
@@ -219,13 +228,14 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     }
   };
 
-  // --- weight rows of this lane: n0 + wc + (lane & 31) + 32j, sub-block half h
+  // --- weight rows of this lane: n0 + wc + (lane & 31) + 32j (SwiGLU: n0 + wc + (lane &
+  // 31) of gate for j = 0 and of up for j = 1), sub-block half h
   const int h = lane >> 5;
   uint32_t row_sub[2], row_sb[2];
   bool rok[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int n = n0 + wc + (lane & 31) + 32 * j;
+    const int n = n0 + wc + (lane & 31) + (sw ? 0 : 32 * j);
     rok[j] = n < N;
     row_sub[j] = rok[j] ? (uint32_t)n * (uint32_t)nsub : 0u;
     row_sb[j] = rok[j] ? (uint32_t)n * (uint32_t)nsb : 0u;
@@ -243,10 +253,10 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     const int sb = 2 * kt + h;
     const bool in = kt < kend && sb < nsub;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) load_raw<QT>(R, row_sub[j], sb, in && rok[j], raw[slot][j]);
+    for (int j = 0; j < 2; ++j) load_raw<QT>(R[j], row_sub[j], sb, in && rok[j], raw[slot][j]);
     if constexpr (is_kquant(QT) && slot % 4 == 0) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) load_hdr<QT>(R, row_sb[j], kt >> 2, in && rok[j], hdr[slot / 4][j]);
+      for (int j = 0; j < 2; ++j) load_hdr<QT>(R[j], row_sb[j], kt >> 2, in && rok[j], hdr[slot / 4][j]);
     }
   };
 
@@ -395,40 +405,51 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   }
   void* const out = p.ws ? (void*)(p.ws + (size_t)split * p.ws_split) : G.y;
   const int yt = p.ws ? DT_F32 : G.y_dtype;
-  if (sw && !p.ws) {
-    // SwiGLU: every wavefront parks its block (bias added) in its LDS area; gate
-    // wavefront w then reads its own block and up's (area w + 2) and stores
-    // swish(gate) * up to y (gate's columns).
-    const float* epu = (const float*)lds + (wave + 2) * (32 * EP_LD);
+  if constexpr (sw) {
+    // SwiGLU (no biases): accumulator v of blocks (i, 0) and (i, 1) holds gate and up of
+    // the same output, m = m0 + 32i + lane%32, n = n0 + 32w + 8(v/4) + 4(lane/32) + v%4.
+    // Per i the wavefront parks the two 32 x 32 blocks in its LDS area and stores whole
+    // row segments of swish(gate) * up (or, split, of both partials): lane l takes columns
+    // 4(l%8) .. +3 of rows l/8 + 8r.
+    const int c8 = lane & 7;
+    const int hcol = n0 + wc + 4 * c8;
+    const bool hvec = (N & 3) == 0 && hcol + 3 < N;
     sfor<MI>([&](auto I_) {
       constexpr int i = decltype(I_)::value;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int cc = 32 * j + 8 * q + 4 * (lane >> 5);
-          float4 v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-          if (G.bias) {
-            const int nc = n0 + wc + cc;
-            v.x += nc + 0 < N ? load_scalar(G.bias, G.bias_dtype, nc + 0) : 0.f;
-            v.y += nc + 1 < N ? load_scalar(G.bias, G.bias_dtype, nc + 1) : 0.f;
-            v.z += nc + 2 < N ? load_scalar(G.bias, G.bias_dtype, nc + 2) : 0.f;
-            v.w += nc + 3 < N ? load_scalar(G.bias, G.bias_dtype, nc + 3) : 0.f;
-          }
-          *(float4*)(ep + (lane & 31) * EP_LD + cc) = v;
-        }
-      __syncthreads();
-      if (wave < 2) {
+      for (int q = 0; q < 4; ++q) {
+        const int cc = 8 * q + 4 * (lane >> 5);  // column of accumulators 4q .. 4q+3
+        *(float4*)(ep + (lane & 31) * EP_LD + cc) =
+            make_float4(acc[i][0][4 * q], acc[i][0][4 * q + 1], acc[i][0][4 * q + 2], acc[i][0][4 * q + 3]);
+        *(float4*)(ep + (lane & 31) * EP_LD + 32 + cc) =
+            make_float4(acc[i][1][4 * q], acc[i][1][4 * q + 1], acc[i][1][4 * q + 2], acc[i][1][4 * q + 3]);
+      }
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll 1
-        for (int r = 0; r < 8; ++r) {
-          const int row = 4 * r + (lane >> 4);
-          const float4 g = *(const float4*)(ep + row * EP_LD + 4 * c4);
-          const float4 u = *(const float4*)(epu + row * EP_LD + 4 * c4);
-          const int m = m0 + 32 * i + row;
-          if (m < M) {
+      for (int r = 0; r < 4; ++r) {
+        const int row = 8 * r + (lane >> 3);
+        const int m = m0 + 32 * i + row;
+        if (m < M) {
+          if (p.ws) {  // split: gate and up partials to columns n and N + n of the workspace
+            float* wrow = p.ws + (size_t)split * p.ws_split + (size_t)m * (size_t)p.ws_ld;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+              const float4 v = *(const float4*)(ep + row * EP_LD + 32 * half + 4 * c8);
+              float* dst = wrow + (size_t)half * N + hcol;
+              if (hvec) {
+                *(float4*)dst = v;
+              } else {
+                const float o[4] = {v.x, v.y, v.z, v.w};
+                for (int e = 0; e < 4; ++e)
+                  if (hcol + e < N) dst[e] = o[e];
+              }
+            }
+          } else {
+            const float4 g = *(const float4*)(ep + row * EP_LD + 4 * c8);
+            const float4 u = *(const float4*)(ep + row * EP_LD + 32 + 4 * c8);
             const float o[4] = {swiglu1(g.x, u.x), swiglu1(g.y, u.y), swiglu1(g.z, u.z), swiglu1(g.w, u.w)};
-            const size_t at = (size_t)m * (size_t)G.ldy + (size_t)ncol;
-            if (vec_ok) {
+            const size_t at = (size_t)m * (size_t)G.ldy + (size_t)hcol;
+            if (hvec) {
               if (yt == DT_F32) *(float4*)((float*)out + at) = make_float4(o[0], o[1], o[2], o[3]);
               else if (yt == DT_BF16)
                 *(uint2*)((uint16_t*)out + at) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
@@ -436,12 +457,12 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
             } else {
 #pragma unroll 1
               for (int e = 0; e < 4; ++e)
-                if (ncol + e < N) store_scalar(out, yt, at + e, o[e]);
+                if (hcol + e < N) store_scalar(out, yt, at + e, o[e]);
             }
           }
         }
       }
-      __syncthreads();
+      __builtin_amdgcn_wave_barrier();
     });
     return;
   }
@@ -478,7 +499,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   });
 }
 
-template <int QT, int XT, int MI>
+template <int QT, int XT, int MI, bool SW>
 hipError_t launch_tile_t(const TileParams& tp, int nblocks, hipStream_t s) {
   // activation stages, or the epilogue's four 32 x 68 fp32 blocks if larger (MI = 2)
   constexpr int lds_bytes = std::max(NSTAGE * 32 * MI * TK * 2, 4 * 32 * 68 * 4);
@@ -488,12 +509,12 @@ hipError_t launch_tile_t(const TileParams& tp, int nblocks, hipStream_t s) {
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   const uint64_t bit = 1ull << (dev & 63);
   if (!(attr_set.load(std::memory_order_acquire) & bit)) {
-    const hipError_t e = hipFuncSetAttribute((const void*)qgemm_tile_kernel<QT, XT, MI>,
+    const hipError_t e = hipFuncSetAttribute((const void*)qgemm_tile_kernel<QT, XT, MI, SW>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes);
     if (e != hipSuccess) return e;
     attr_set.fetch_or(bit, std::memory_order_release);
   }
-  qgemm_tile_kernel<QT, XT, MI><<<dim3((unsigned)nblocks), dim3(256), lds_bytes, s>>>(tp);
+  qgemm_tile_kernel<QT, XT, MI, SW><<<dim3((unsigned)nblocks), dim3(256), lds_bytes, s>>>(tp);
   return hipGetLastError();
 }
 
@@ -502,8 +523,14 @@ template <int QT, int XT>
 hipError_t launch_q(TileParams tp, int bm, int S, hipStream_t s) {
   tp.tiles_m = (tp.M + bm - 1) / bm;
   const int ntiles = tp.tiles_m * tp.tiles_n;
-  if (bm == 64) return launch_tile_t<QT, XT, 2>(tp, ntiles * S, s);
-  return bm == 128 ? launch_tile_t<QT, XT, 4>(tp, ntiles * S, s) : launch_tile_t<QT, XT, 8>(tp, ntiles * S, s);
+  if (tp.swiglu) {
+    if (bm == 64) return launch_tile_t<QT, XT, 2, true>(tp, ntiles * S, s);
+    return bm == 128 ? launch_tile_t<QT, XT, 4, true>(tp, ntiles * S, s)
+                     : launch_tile_t<QT, XT, 8, true>(tp, ntiles * S, s);
+  }
+  if (bm == 64) return launch_tile_t<QT, XT, 2, false>(tp, ntiles * S, s);
+  return bm == 128 ? launch_tile_t<QT, XT, 4, false>(tp, ntiles * S, s)
+                   : launch_tile_t<QT, XT, 8, false>(tp, ntiles * S, s);
 }
 
 // One translation unit per quant type instantiates the kernels (qgemm_tile_<type>.hip);

@@ -70,6 +70,7 @@ _SIGS = {
     "mlxr_qgemm_run_ex": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_workspace_size": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_size_t)]),
     "mlxr_qgemm_run_ws": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mlxr_bench_stream_read": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run_noalloc": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p] * 2 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_swiglu_workspace_size": (ctypes.c_int, [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_size_t)]),
     "mlxr_qgemm_swiglu": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
@@ -191,20 +192,45 @@ class PackedWeight:
 
 
 def pack_weights(gguf, N, K, qtype, device="cuda", stream=None):
-    """One-time upload of GGUF blocks (numpy/CPU tensor/device tensor) to the packed layout."""
+    """One-time upload of GGUF blocks (numpy/CPU tensor/device tensor) to the packed layout.
+
+    The packed buffer and any device staging copy are allocated on the stream the pack runs
+    on (torch's stream-ordered allocator), so a staging copy freed on return is reused only
+    after the pack."""
     torch = _torch()
-    buf = torch.empty(packed_size(qtype, N, K), dtype=torch.uint8, device=device)
     need = gguf_size(qtype, N, K)
     if isinstance(gguf, np.ndarray):
         gguf = torch.from_numpy(np.ascontiguousarray(gguf).view(np.uint8).reshape(-1))
     if gguf.numel() * gguf.element_size() < need:
         raise QGemmError(-1, "weights buffer is smaller than N * K/group * sizeof(block)")
-    if gguf.device.type == "cpu":
-        gguf = gguf.to(device, non_blocking=False)
-    _check(lib().mlxr_qgemm_pack_device(int(qtype), N, K, gguf.data_ptr(), buf.data_ptr(), _stream_ptr(stream)))
+    with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+        buf = torch.empty(packed_size(qtype, N, K), dtype=torch.uint8, device=device)
+        if gguf.device.type == "cpu":
+            gguf = gguf.to(device, non_blocking=False)
+        elif not gguf.is_contiguous():
+            gguf = gguf.contiguous()
+        _check(lib().mlxr_qgemm_pack_device(int(qtype), N, K, gguf.data_ptr(), buf.data_ptr(), _stream_ptr(stream)))
     if stream is None:
-        torch.cuda.current_stream().synchronize()  # the staging tensor may be freed after return
+        torch.cuda.current_stream().synchronize()  # one-time upload: done when it returns
     return PackedWeight(buf, qtype, N, K)
+
+
+def _check_out(t, M, N, device, what="out"):
+    """A caller's output tensor: contiguous [M, N] fp32/fp16/bf16 on the input's device."""
+    torch = _torch()
+    if tuple(t.shape) != (M, N) or not t.is_contiguous() or t.device != device or \
+            t.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise QGemmError(-1, f"{what} must be a contiguous [{M}, {N}] float32/float16/bfloat16 tensor on {device}")
+
+
+def _check_bias(b, N, device):
+    if b is None:
+        return None
+    if b.dim() != 1 or b.shape[0] != N:
+        raise QGemmError(-3, "Bias shape must be [N]")
+    if b.device != device:
+        raise QGemmError(-1, f"bias must be on {device}")
+    return b.contiguous()
 
 
 def dequantize(pw, dtype=None, stream=None):
@@ -228,8 +254,7 @@ def q_gemm_dequant(input, weights, M, N, K, quant_type, group_size=0, bias=None,
     torch = _torch()
     if input.dim() != 2 or input.shape[0] != M or input.shape[1] != K:
         raise QGemmError(-3, "Input shape must be [M, K]")
-    if bias is not None and (bias.dim() != 1 or bias.shape[0] != N):
-        raise QGemmError(-3, "Bias shape must be [N]")
+    bias = _check_bias(bias, N, input.device)
     if not isinstance(weights, PackedWeight):
         weights = pack_weights(weights, N, K, quant_type, device=input.device, stream=stream)
     elif (weights.qtype, weights.N, weights.K) != (QuantType(quant_type), N, K):
@@ -238,6 +263,7 @@ def q_gemm_dequant(input, weights, M, N, K, quant_type, group_size=0, bias=None,
         input = input.contiguous()
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype or input.dtype, device=input.device)
+    _check_out(out, M, N, input.device)
     # split-K workspace from torch's stream-ordered caching allocator (graph-capture safe)
     ws_bytes = workspace_size(quant_type, N, K, M) if path != PATH_GEMV else 0
     ws = None
@@ -273,10 +299,14 @@ def q_gemm_dequant_grouped(input, weights, outs=None, biases=None, out_dtype=Non
     biases = biases or [None] * n
     if outs is None:
         outs = [torch.empty((M, w.N), dtype=out_dtype or input.dtype, device=input.device) for w in weights]
+    if len(outs) != n or len(biases) != n:
+        raise QGemmError(-1, "one output and one bias (or None) per weight")
+    biases = [_check_bias(b, w.N, input.device) for w, b in zip(weights, biases)]
     arr = (Item * n)()
     for i, (w, y, b) in enumerate(zip(weights, outs, biases)):
         if w.K != K:
             raise QGemmError(-3, "Input shape must be [M, K]")
+        _check_out(y, M, w.N, input.device, f"outs[{i}]")
         arr[i] = Item(int(w.qtype), w.N, w.K, 0, w.data_ptr(), b.data_ptr() if b is not None else None,
                       _dt_code(b.dtype) if b is not None else F32, y.data_ptr(), _dt_code(y.dtype))
     if not workspace:
@@ -306,6 +336,7 @@ def q_gemm_swiglu(input, gate, up, out=None, out_dtype=None, stream=None, worksp
         input = input.contiguous()
     if out is None:
         out = torch.empty((M, gate.N), dtype=out_dtype or input.dtype, device=input.device)
+    _check_out(out, M, gate.N, input.device)
     n = ctypes.c_size_t(0)
     _check(lib().mlxr_qgemm_swiglu_workspace_size(int(gate.qtype), gate.N, K, M, _dt_code(out.dtype), ctypes.byref(n)))
     ws = None

@@ -312,6 +312,31 @@ def test_mfma_chunked_launches(cuda, monkeypatch):
     assert orc.rel_err(y1.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("M", [8, 40])
+def test_skinny_operand_limit_falls_back_to_chunked_tiles(cuda, monkeypatch, M):
+    """The skinny kernels address every operand with 32-bit offsets: when a weight plane
+    reaches the limit (lowered here so that a small shape does) the call runs on the tiled
+    kernel's chunked launches instead, and stays within tolerance; grouped calls and the
+    fused SwiGLU fall back the same way."""
+    import torch
+    qt, N, K = Q4K, 700, 1024
+    w, pw = _packed(torch, qt, N, K, 151 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 152 + M, cuda)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
+    y1 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    monkeypatch.setenv("MLXR_MFMA_CHUNK_BYTES", str(1 << 17))  # below the 358 KB qs plane
+    y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    ys = mx.q_gemm_dequant_grouped(x, [pw, pw], out_dtype=torch.float32)
+    for y in (y1, y2, ys[0], ys[1]):
+        assert orc.rel_err(y.cpu().numpy(), ref) <= TOL
+    wu = mx.synth_gguf(qt, N, K, 161 + M)
+    pu = mx.pack_weights(wu, N, K, qt, device=cuda)
+    h = mx.q_gemm_swiglu(x, pw, pu, out_dtype=torch.float32)
+    g = ref.astype(np.float64)
+    u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=True).astype(np.float64)
+    assert orc.rel_err(h.cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= TOL
+
+
 # The skinny kernel's narrow (16x16x32) variant on Q4_K: ragged N, K shorter than or not a
 # multiple of its ring (steps of 128), both activation dtypes, M from 1 to 16.
 @pytest.mark.parametrize("M,N,K,xdt", [(5, 100, 768, mx.BF16), (8, 1000, 2304, mx.F16), (9, 257, 4096, mx.BF16),
@@ -376,3 +401,23 @@ def test_mfma_split_k(cuda, qt, M, N, K, ydt):
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bias.float().cpu().numpy(), w_to_bf16=True)
     for y in (ys[0], ys[3]):
         assert orc.rel_err(y.float().cpu().numpy(), ref) <= TOL
+
+
+def test_python_binding_checks_outputs_and_bias(cuda):
+    """Caller-supplied outputs must be contiguous [M, N] tensors on the input's device (the
+    kernels write M*N elements); biases must be [N] on that device."""
+    import torch
+    qt, M, N, K = Q4K, 3, 64, 256
+    w, pw = _packed(torch, qt, N, K, 171, cuda)
+    x, _ = _act(torch, M, K, mx.BF16, 172, cuda)
+    for bad in (torch.empty((M, N - 1), device=cuda), torch.empty((N, M), device=cuda).t(),
+                torch.empty((M, N)), torch.empty((M, N), dtype=torch.int32, device=cuda)):
+        with pytest.raises(mx.QGemmError):
+            mx.q_gemm_dequant(x, pw, M, N, K, qt, out=bad)
+        with pytest.raises(mx.QGemmError):
+            mx.q_gemm_dequant_grouped(x, [pw], outs=[bad])
+    with pytest.raises(mx.QGemmError):
+        mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=torch.zeros(N))  # host bias
+    strided = torch.zeros(2 * N, device=cuda)[::2]
+    y = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=strided, out_dtype=torch.float32)
+    assert torch.equal(y, mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32))
