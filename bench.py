@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--skip-dropin", action="store_true",
                     help="do not time the seven-call drop-in step (profiler runs of the headline kernel)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
-                    help="after the headline, run one device copy of this many MB (profiler calibration)")
+                    help="at the end, run one device copy of this many MB (profiler calibration)")
     return ap.parse_args()
 
 
@@ -292,13 +292,6 @@ def run_headline(cx, args, out):
         step7(copies[len(graphs) - 1])
         torch.cuda.synchronize()
         grouped_ok = all(torch.equal(y_g[n], ys[n]) for n in ys)
-
-    if args.calib_copy_mb:
-        nb = args.calib_copy_mb * 1000000
-        src = torch.empty(nb, dtype=torch.uint8, device=cx.dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
 
     # accuracy of one layer of the step (as the graph ran it): every output
     step(copies[0])
@@ -646,6 +639,13 @@ def main():
             torch.cuda.empty_cache()
     if configs:
         out["configs"] = configs
+    if args.calib_copy_mb:
+        # one device copy of a known size, for scaling the profiler's traffic counters
+        nb = args.calib_copy_mb * 1000000
+        src = torch.empty(nb, dtype=torch.uint8, device=cx.dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(out))
 
 

@@ -187,6 +187,13 @@ __device__ __forceinline__ void dequant_raw(const RawSub<QT>& r, int j, float* w
   }
 }
 
+// (v & mask) | bits in one VALU op; the compiler otherwise emits an and plus an or.
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(bits));
+  return r;
+}
+
 // swish(g) * u = g / (1 + exp(-g)) * u in fp32: the gating of the SwiGLU MLP
 // (reference core/graph/layers.cpp:391-414).
 __device__ __forceinline__ float swiglu1(float g, float u) { return g / (1.f + __expf(-g)) * u; }

@@ -447,12 +447,6 @@ struct CLoad<QT_Q4_1> {
   uint32_t d;
 };
 
-// (v & mask) | bits in one VALU op; the compiler otherwise emits an and plus an or.
-__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bits) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(mask), "v"(bits));
-  return r;
-}
 
 // One weight of a (possibly grouped) launch.  Weights in one launch share K, the quant
 // type and the activations; each owns a contiguous range of wavefronts.

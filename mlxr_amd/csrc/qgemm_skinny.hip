@@ -576,8 +576,11 @@ hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   const void* const bias = sp.bias;
   if (pl.ks == 1) sp.ws = nullptr;
   const dim3 grid((unsigned)(sp.slabs * pl.ks)), block((unsigned)(64 * pl.w));
-  if (sp.M <= 16) qgemm_skinny16_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
-  else qgemm_skinny16_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);
+  if (sp.M <= 16) {
+    qgemm_skinny16_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
+  } else {
+    qgemm_skinny16_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || pl.ks == 1) return e;
   if (sp.swiglu)
