@@ -34,9 +34,9 @@ int device_cus() {
 // tile step: a 128-row tile step costs 0.64 of it (the weight dequant is shared by half
 // the rows); a round of workgroups costs its steps plus 0.8 (prologue, epilogue); a
 // split launch adds the reduce kernel, about 3 us plus its partial-sum traffic at
-// ~5 TB/s (one 256-row step is ~1.86 us).  Splits are whole groups of four steps (a
-// super-block), at least eight steps each, at most eight splits, and only with a
-// workspace of S*M*N*4 bytes.  MLXR_MFMA_BM / MLXR_MFMA_SPLIT force a choice.
+// ~5 TB/s (one 256-row step is ~1.86 us).  Splits are whole groups of eight steps (two
+// super-blocks: the kernel's loop runs whole rings of eight steps), at most eight splits,
+// and only with a workspace of S*M*N*4 bytes.
 struct SplitPlan {
   int bm, tiles, S, kps;
 };
@@ -48,7 +48,7 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
   for (int bm : {256, 128, 64}) {
     const long tiles = ((M + bm - 1) / bm) * tn;
     for (int S = 1; S <= 8; ++S) {
-      const int kps = (((nkt + S - 1) / S) + 3) / 4 * 4;
+      const int kps = (((nkt + S - 1) / S) + 7) / 8 * 8;
       const int Sr = (nkt + kps - 1) / kps;  // splits actually used
       if (Sr != S) continue;
       if (S > 1 && (kps < 8 || (size_t)S * (size_t)M * (size_t)N * 4u > ws_bytes)) continue;

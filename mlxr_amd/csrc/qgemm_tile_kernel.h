@@ -371,11 +371,15 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     issue_raw(kt + PD, U);
   };
 
+  // Whole rings of PD steps, unconditionally: steps past kend load nothing (out-of-range
+  // offsets: zero activations and zero weights, so they add zeros) and the loop body is one
+  // straight-line path.  (With the steps past kend skipped by branches inside the body, the
+  // compiler could not carry its load wait counts across the back edge and drained every
+  // load, the prefetches included, at each trip.)
   for (int kt = kt0; kt < kend; kt += PD) {
-    step(kt, std::integral_constant<int, 0>());
-    sfor<PD - 1>([&](auto U_) {
-      constexpr int u = decltype(U_)::value + 1;
-      if (kt + u < kend) step(kt + u, std::integral_constant<int, u>());
+    sfor<PD>([&](auto U_) {
+      constexpr int u = decltype(U_)::value;
+      step(kt + u, std::integral_constant<int, u>());
     });
   }
 
