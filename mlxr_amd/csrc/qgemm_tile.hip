@@ -190,7 +190,6 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   }
   if (sp.S > 1) {
     TileParams tp;
-  tp.swiglu = 0;
     tp.swiglu = 0;
     tp.M = M;
     tp.K = K;
@@ -223,9 +222,7 @@ hipError_t launch_mfma(const RunArgs& a, hipStream_t s) {
   for (int mc = 0; mc < M; mc += Mc) {
     for (int nc = 0; nc < N; nc += Nc) {
       TileParams tp;
-  tp.swiglu = 0;
       tp.swiglu = 0;
-    tp.swiglu = 0;
       tp.M = std::min(Mc, M - mc);
       tp.K = K;
       tp.x = (const uint8_t*)a.x + (size_t)mc * K * 2;

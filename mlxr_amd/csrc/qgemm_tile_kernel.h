@@ -207,25 +207,26 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   const i32x4_t rx = make_srsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
   // Always MI DMA instructions per wavefront and step (steps past the end read zeros
   // into a stage nobody reads), so the wait counts below are exact.
-  auto issue_a = [&](int kt) {
+  auto issue_a1 = [&](int kt, int i) {
     const bool live = kt < kend;
     const bool last_half = ktail != 0 && kt == nkt - 1;  // ktail is 32 here
     const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane(kt * (TK * 2));
     const uint32_t dst = lds_base + (uint32_t)((kt & (NSTAGE - 1)) * A_STAGE + wave * MI * 1024);
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const uint32_t vo = (live && !(last_half && a_hi[i])) ? a_voff[i] : OOB;
-      const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + i * 1024));
-      // M0 holds the LDS destination; nothing else in this kernel uses M0 (DS
-      // instructions on gfx9+ do not), so clobbering it is safe here.
+    const uint32_t vo = (live && !(last_half && a_hi[i])) ? a_voff[i] : OOB;
+    const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)(dst + i * 1024));
+    // M0 holds the LDS destination; nothing else in this kernel uses M0 (DS
+    // instructions on gfx9+ do not), so clobbering it is safe here.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-      asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-                   :
-                   : "v"(vo), "s"(rx), "s"(soff), "s"(m0v)
-                   : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(vo), "s"(rx), "s"(soff), "s"(m0v)
+                 : "memory", "m0");
 #pragma clang diagnostic pop
-    }
+  };
+  auto issue_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) issue_a1(kt, i);
   };
 
   // --- weight rows of this lane: n0 + wc + (lane & 31) + 32j (SwiGLU: n0 + wc + (lane &
@@ -292,8 +293,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
     return *(const uint4*)(lds + stage * A_STAGE + r * 128 + c * 16);
   };
 
-  // ---- prologue.  Steady state issues, in step s: the DMA of stage s+3 half way and the
-  // raw loads of step s+PD at the end.  The prologue issues raw loads of steps
+  // ---- prologue.  Steady state issues, in step s: the DMA of stage s+3 over the second
+  // half and the raw loads of step s+PD at the end.  The prologue issues raw loads of steps
   // 0 .. PD-3, the DMAs of stages 0 and 1, raw PD-2, DMA 2, raw PD-1: after the DMA of
   // any stage k, exactly raw(k+PD-2), DMA(k+1), raw(k+PD-1) follow, as in the loop.
   sfor<PD - 2>([&](auto S_) {
@@ -329,8 +330,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   // the slice's SPS slots; the finished words replace bf[.][kk] after the slice's last
   // MFMA.  Half way the wavefront waits for its DMA of stage kt+1 and joins the
   // barrier: then stage kt+1 is complete and stage kt-1 free, so the DMA of step kt+3
-  // goes into it.  The raw weights of step kt+4 are loaded at the end, into the ring
-  // slot step kt just used.
+  // goes into it, over the second half.  The raw weights of step kt+PD are loaded at the
+  // end, into the ring slot step kt just used.
   auto step = [&](int kt, auto U) {
     constexpr int u = decltype(U)::value;      // (kt - kt0) % PD; LDS stage u % 4
     constexpr int un = (u + 1) % PD;
@@ -350,8 +351,11 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
         // kt+PD-1
         vm_wait<MI + rops((u + PD - 2) % PD) + rops((u + PD - 1) % PD)>();
         __syncthreads();
-        issue_a(kt + NSTAGE - 1);
       }
+      // the DMA of step kt+3, one instruction every third slot of the second half (issued
+      // all at once right after the barrier, by all four wavefronts, they were 2-4% slower)
+      if constexpr (m >= NSLOT / 2 && (m - NSLOT / 2) % 3 == 0 && (m - NSLOT / 2) / 3 < MI)
+        issue_a1(kt + NSTAGE - 1, (m - NSLOT / 2) / 3);
       // tasks k = 0..9 of the slice (0: prelude row 0, 1-4: its quarters, 5: prelude
       // row 1, 6-9: its quarters); task k runs in slot (k * SPS) / 10
       sfor<10>([&](auto TK_) {
@@ -407,6 +411,11 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) bv[e] = ncol + e < N ? load_scalar(G.bias, G.bias_dtype, ncol + e) : 0.f;
   }
+  // Take the bias values here, once: with their loads still pending at the row loops
+  // below, the compiler waited for every outstanding memory operation, the previous
+  // block's stores included, at the start of each of the MI blocks.
+#pragma unroll
+  for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(bv[e]));
   void* const out = p.ws ? (void*)(p.ws + (size_t)split * p.ws_split) : G.y;
   const int yt = p.ws ? DT_F32 : G.y_dtype;
   if constexpr (sw) {
@@ -429,40 +438,67 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
             make_float4(acc[i][1][4 * q], acc[i][1][4 * q + 1], acc[i][1][4 * q + 2], acc[i][1][4 * q + 3]);
       }
       __builtin_amdgcn_wave_barrier();
-#pragma unroll 1
-      for (int r = 0; r < 4; ++r) {
-        const int row = 8 * r + (lane >> 3);
-        const int m = m0 + 32 * i + row;
-        if (m < M) {
-          if (p.ws) {  // split: gate and up partials to columns n and N + n of the workspace
-            float* wrow = p.ws + (size_t)split * p.ws_split + (size_t)m * (size_t)p.ws_ld;
+      // lane l: rows mb + 8r (r = 0..3), gate and up of its four columns; all reads first
+      float4 g[4], u[4];
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-              const float4 v = *(const float4*)(ep + row * EP_LD + 32 * half + 4 * c8);
-              float* dst = wrow + (size_t)half * N + hcol;
-              if (hvec) {
-                *(float4*)dst = v;
-              } else {
-                const float o[4] = {v.x, v.y, v.z, v.w};
-                for (int e = 0; e < 4; ++e)
-                  if (hcol + e < N) dst[e] = o[e];
+      for (int r = 0; r < 4; ++r) {
+        g[r] = *(const float4*)(ep + (8 * r + (lane >> 3)) * EP_LD + 4 * c8);
+        u[r] = *(const float4*)(ep + (8 * r + (lane >> 3)) * EP_LD + 32 + 4 * c8);
+      }
+      const int mb = m0 + 32 * i + (lane >> 3);
+      const bool full = hvec && m0 + 32 * i + 32 <= M;
+      if (p.ws) {  // split: gate and up partials to columns n and N + n of the workspace
+        float* const w0 = p.ws + (size_t)split * p.ws_split + (size_t)mb * (size_t)p.ws_ld + hcol;
+        const size_t rs = 8 * (size_t)p.ws_ld;
+        if (full) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            *(float4*)(w0 + r * rs) = g[r];
+            *(float4*)(w0 + r * rs + N) = u[r];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (mb + 8 * r >= M) continue;
+            const float og[4] = {g[r].x, g[r].y, g[r].z, g[r].w}, ou[4] = {u[r].x, u[r].y, u[r].z, u[r].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (hcol + e < N) {
+                w0[r * rs + e] = og[e];
+                w0[r * rs + N + e] = ou[e];
               }
-            }
+          }
+        }
+      } else {
+        float4 o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          o[r] = make_float4(swiglu1(g[r].x, u[r].x), swiglu1(g[r].y, u[r].y), swiglu1(g[r].z, u[r].z),
+                             swiglu1(g[r].w, u[r].w));
+        const size_t at0 = (size_t)mb * (size_t)G.ldy + (size_t)hcol, rs = 8 * (size_t)G.ldy;
+        if (full) {
+          if (yt == DT_BF16) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              *(uint2*)((uint16_t*)out + at0 + r * rs) =
+                  make_uint2(pack_bf16x2(o[r].x, o[r].y), pack_bf16x2(o[r].z, o[r].w));
+          } else if (yt == DT_F32) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) *(float4*)((float*)out + at0 + r * rs) = o[r];
           } else {
-            const float4 g = *(const float4*)(ep + row * EP_LD + 4 * c8);
-            const float4 u = *(const float4*)(ep + row * EP_LD + 32 + 4 * c8);
-            const float o[4] = {swiglu1(g.x, u.x), swiglu1(g.y, u.y), swiglu1(g.z, u.z), swiglu1(g.w, u.w)};
-            const size_t at = (size_t)m * (size_t)G.ldy + (size_t)hcol;
-            if (hvec) {
-              if (yt == DT_F32) *(float4*)((float*)out + at) = make_float4(o[0], o[1], o[2], o[3]);
-              else if (yt == DT_BF16)
-                *(uint2*)((uint16_t*)out + at) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-              else *(uint2*)((uint16_t*)out + at) = make_uint2(pack2<X_F16>(o[0], o[1]), pack2<X_F16>(o[2], o[3]));
-            } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              *(uint2*)((uint16_t*)out + at0 + r * rs) =
+                  make_uint2(pack2<X_F16>(o[r].x, o[r].y), pack2<X_F16>(o[r].z, o[r].w));
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (mb + 8 * r >= M) continue;
+            const float oe[4] = {o[r].x, o[r].y, o[r].z, o[r].w};
 #pragma unroll 1
-              for (int e = 0; e < 4; ++e)
-                if (hcol + e < N) store_scalar(out, yt, at + e, o[e]);
-            }
+            for (int e = 0; e < 4; ++e)
+              if (hcol + e < N) store_scalar(out, yt, at0 + r * rs + e, oe[e]);
           }
         }
       }
@@ -479,24 +515,39 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
         *(float4*)(ep + (lane & 31) * EP_LD + 32 * j + 8 * q + 4 * (lane >> 5)) =
             make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
     __builtin_amdgcn_wave_barrier();
-#pragma unroll 1
+    // all eight row reads first, one wait, then the stores: lane l holds rows
+    // mb + 4r (r = 0..7) of its four columns
+    float4 v[8];
+#pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const int row = 4 * r + (lane >> 4);
-      const float4 v = *(const float4*)(ep + row * EP_LD + 4 * c4);
-      const int m = m0 + 32 * i + row;
-      if (m < M) {
-        const float o[4] = {v.x + bv[0], v.y + bv[1], v.z + bv[2], v.w + bv[3]};
-        const size_t at = (size_t)m * (size_t)ld + (size_t)(cb + ncol);
-        if (vec_ok) {
-          if (yt == DT_F32) *(float4*)((float*)out + at) = make_float4(o[0], o[1], o[2], o[3]);
-          else if (yt == DT_BF16)
-            *(uint2*)((uint16_t*)out + at) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-          else *(uint2*)((uint16_t*)out + at) = make_uint2(pack2<X_F16>(o[0], o[1]), pack2<X_F16>(o[2], o[3]));
-        } else {
+      v[r] = *(const float4*)(ep + (4 * r + (lane >> 4)) * EP_LD + 4 * c4);
+      v[r] = make_float4(v[r].x + bv[0], v[r].y + bv[1], v[r].z + bv[2], v[r].w + bv[3]);
+    }
+    const int mb = m0 + 32 * i + (lane >> 4);
+    const size_t at0 = (size_t)mb * (size_t)ld + (size_t)(cb + ncol), rs = 4 * (size_t)ld;
+    if (vec_ok && m0 + 32 * i + 32 <= M) {  // whole block in range: straight-line stores
+      if (yt == DT_BF16) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          *(uint2*)((uint16_t*)out + at0 + r * rs) =
+              make_uint2(pack_bf16x2(v[r].x, v[r].y), pack_bf16x2(v[r].z, v[r].w));
+      } else if (yt == DT_F32) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) *(float4*)((float*)out + at0 + r * rs) = v[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          *(uint2*)((uint16_t*)out + at0 + r * rs) =
+              make_uint2(pack2<X_F16>(v[r].x, v[r].y), pack2<X_F16>(v[r].z, v[r].w));
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        if (mb + 4 * r >= M) continue;
+        const float o[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
 #pragma unroll 1
-          for (int e = 0; e < 4; ++e)
-            if (ncol + e < N) store_scalar(out, yt, at + e, o[e]);
-        }
+        for (int e = 0; e < 4; ++e)
+          if (ncol + e < N) store_scalar(out, yt, at0 + r * rs + e, o[e]);
       }
     }
     __builtin_amdgcn_wave_barrier();

@@ -70,9 +70,9 @@ def test_noalloc_without_split_and_too_large(cuda):
     y0 = _run(torch, True, pw, x, N, K, 1)
     y1 = _run(torch, False, pw, x, N, K, 1, torch.empty(16, dtype=torch.uint8, device=cuda))
     assert torch.equal(y0, y1)
-    # a plan needing more than the array (Llama-3-8B down at M = 512 splits K eight
+    # a plan needing more than the array (Llama-3-8B down at M = 1024 splits K four
     # ways: 64 MiB of partials): a clear error, nothing launched
-    N2, K2, M2 = 4096, 14336, 512
+    N2, K2, M2 = 4096, 14336, 1024
     assert _need(N2, K2, M2) > SCRATCH
     pw2 = mx.pack_weights(mx.synth_gguf(Q4K, N2, K2, 8), N2, K2, Q4K, device=cuda)
     x2 = _x(torch, M2, K2, 14, cuda)
