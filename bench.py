@@ -168,27 +168,29 @@ def worst(errs):
 
 # ------------------------------------------------------------------------------ headline
 
-def stream_read_step_ms(cx, args, step_launches):
-    """Graph-replayed time of a step whose launches only stream-read the given packed
-    weights: step_launches = [[[PackedWeight, ...] per launch] per layer]."""
+def stream_read_ms(cx, args, launches):
+    """Graph-replayed time of a sequence of launches that only stream-read the given packed
+    weights (launches = [[PackedWeight, ...] per launch], one mlxr_bench_stream_read each):
+    milliseconds per replay of the whole sequence.  Grid: 2048 workgroups (fewer for a
+    launch under 8 MB), the best of the grid sizes tried on MI355X for these buffers
+    (256 .. 16384 workgroups, per launch kind and for the whole step)."""
     import ctypes
     mx, torch = cx.mx, cx.torch
     sink = torch.zeros(1024, dtype=torch.int32, device=cx.dev)
     calls = []
-    for layer in step_launches:
-        for pws in layer:
-            ptrs = (ctypes.c_void_p * len(pws))(*[pw.data_ptr() for pw in pws])
-            sizes = (ctypes.c_size_t * len(pws))(*[pw.nbytes for pw in pws])
-            grid = int(min(-(-sum(pw.nbytes for pw in pws) // (16 * 1024)), 2048))
-            calls.append((len(pws), ptrs, sizes, grid))
+    for pws in launches:
+        ptrs = (ctypes.c_void_p * len(pws))(*[pw.data_ptr() for pw in pws])
+        sizes = (ctypes.c_size_t * len(pws))(*[pw.nbytes for pw in pws])
+        grid = int(min(-(-sum(pw.nbytes for pw in pws) // 4096), 2048))
+        calls.append((len(pws), ptrs, sizes, grid))
     lib = mx.qgemm.lib()
 
-    def step():
+    def seq():
         st = mx.qgemm._stream_ptr(None)
         for n, ptrs, sizes, grid in calls:
             mx.qgemm._check(lib.mlxr_bench_stream_read(n, ptrs, sizes, sink.data_ptr(), grid, st))
 
-    g = cx.graph(step)
+    g = cx.graph(seq)
     for _ in range(args.warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -271,7 +273,10 @@ def run_headline(cx, args, out):
     # the same step's launch structure with a pure streaming read of the same packed weight
     # buffers in place of each GEMV launch (mlxr_bench_stream_read): the HBM ceiling of
     # 4 launches per layer, 128 per step, in one graph
-    ms_ceiling = stream_read_step_ms(cx, args, [[[W[n] for n in names] for _, names in LAUNCHES] for W in copies])
+    ms_ceiling = stream_read_ms(cx, args, [[W[n] for n in names] for W in copies for _, names in LAUNCHES])
+    # and per launch kind: R back-to-back reads of one kind's buffers (as kern_us above)
+    read_us = {lname: 1e3 * stream_read_ms(cx, args, [[copies[r % len(copies)][n] for n in names] for r in range(R)]) / R
+               for lname, names in LAUNCHES}
     # one layer per graph (a graph launch per 4 kernels), for comparison
     graphs = [cx.graph(lambda W=W: step(W)) for W in copies[:8]]
     for c in range(args.warmup):
@@ -326,7 +331,9 @@ def run_headline(cx, args, out):
             "one_layer_graph_GBps": round(step_bytes / (ms_graph * 1e-3) / 1e9, 1),
             "launches": {ln: {"us": round(kern_us[ln], 3), "bytes": lbytes[ln],
                               "GBps": round(lbytes[ln] / (kern_us[ln] * 1e-6) / 1e9, 1),
-                              "frac_hbm": round(lbytes[ln] / (kern_us[ln] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                              "frac_hbm": round(lbytes[ln] / (kern_us[ln] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                              "stream_read_us": round(read_us[ln], 3),
+                              "vs_stream_read": round(read_us[ln] / kern_us[ln], 4)}
                          for ln, _ in LAUNCHES},
             "warm_launches_infinity_cache": {ln: {"us": round(warm_us[ln], 3),
                                                   "GBps": round(lbytes[ln] / (warm_us[ln] * 1e-6) / 1e9, 1)}
@@ -482,6 +489,21 @@ def run_c4(cx, args):
     fn(0)
     us = 1e3 * cx.graph_ms(fn, 5)
     res["plain_bf16_gemm_library_M2048_gate"] = {"us": round(us, 1), "TFLOPs": round(2.0 * M * N * K / us / 1e6, 1)}
+    # ceiling: back-to-back bf16 MFMAs from registers on every SIMD, no memory traffic
+    # (mlxr_bench_mfma_peak) -- the rate the matrix cores sustain here, clock throttling
+    # under full load included
+    cus = torch.cuda.get_device_properties(cx.dev).multi_processor_count
+    iters = 1024
+    out = torch.empty(cus * 256, dtype=torch.float32, device=cx.dev)
+    lib = mx.qgemm.lib()
+    fn = lambda r: mx.qgemm._check(lib.mlxr_bench_mfma_peak(cus, iters, out.data_ptr(),
+                                                             torch.cuda.current_stream().cuda_stream))
+    fn(0)
+    us = 1e3 * cx.graph_ms(fn, 4)
+    tf = cus * 4 * iters * 16 * 32768 / us / 1e6
+    res["mfma_ceiling"] = {"TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+                           "c4_M2048_vs_ceiling": round(res["M=2048"]["TFLOPs"] / tf, 4),
+                           "c4_M2048_layer_vs_ceiling": round(res["M=2048"]["layer_grouped_4_calls"]["TFLOPs"] / tf, 4)}
     return res
 
 

@@ -217,6 +217,13 @@ int mlxr_swiglu(const void* gate_dev, const void* up_dev, void* out_dev, size_t 
 int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const size_t* bytes, void* sink_dev, int grid,
                            void* stream);
 
+/* Benchmark probe: grid workgroups of four wavefronts (one per SIMD), each issuing
+ * iters x 16 independent bf16 32x32x16 MFMAs from registers, no memory traffic; writes
+ * grid * 256 floats to out_dev.  Flops per launch = grid * 4 * iters * 16 * 32768.  bench.py
+ * times it as the matrix-core rate the part sustains under full load (the prefill GEMMs'
+ * ceiling).  No counterpart in the reference. */
+int mlxr_bench_mfma_peak(int grid, int iters, void* out_dev, void* stream);
+
 /* Deterministic synthetic inputs with the shapes/distributions of the benchmark
  * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by
  * Box-Muller in double precision.

@@ -1,8 +1,12 @@
-// Measurement kernel for the benchmark (not part of the matmul path): a pure streaming
-// read of up to four device buffers in one launch, the bytes a grouped GEMV launch reads,
-// with nothing computed on them.  bench.py runs it over the headline step's packed weights
-// in the step's launch structure (one launch per grouped projection, one graph) to give
-// the HBM ceiling that structure allows.
+// Measurement kernels for the benchmark (not part of the matmul path).
+//  - stream_read_kernel: a pure streaming read of up to four device buffers in one launch,
+//    the bytes a grouped GEMV launch reads, with nothing computed on them.  bench.py runs
+//    it over the headline step's packed weights in the step's launch structure (one launch
+//    per grouped projection, one graph) to give the HBM ceiling that structure allows.
+//  - mfma_peak_kernel: back-to-back independent bf16 MFMAs (32x32x16, sixteen
+//    accumulators per wavefront, one wavefront per SIMD), nothing loaded: the matrix-core
+//    rate the chip sustains under full load, clock throttling included, as the ceiling of
+//    the prefill GEMMs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -51,8 +55,46 @@ __global__ __launch_bounds__(256) void stream_read_kernel(ReadParams rp) {
   if (acc == 0x9E3779B9u && threadIdx.x == 0) rp.sink[blockIdx.x & 1023] = acc;
 }
 
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Each wavefront: iters x 16 MFMAs on sixteen independent accumulators; operands from
+// registers (small values, so nothing overflows); the sums go to out (one float per
+// thread) so nothing is dropped.
+__global__ __launch_bounds__(256, 1) void mfma_peak_kernel(float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t va = 0x3c003c00u ^ (uint32_t)(lane * 0x00010001u), vb = va ^ 0x00400040u;
+  const u32x4_t a = {va, va ^ 0x10001u, va ^ 0x20002u, va ^ 0x30003u};
+  const u32x4_t b = {vb, vb ^ 0x10001u, vb ^ 0x20002u, vb ^ 0x30003u};
+  f32x16_t acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                       acc[i], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += acc[i][v];
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 }  // namespace
 }  // namespace mlxr
+
+extern "C" int mlxr_bench_mfma_peak(int grid, int iters, void* out_dev, void* stream) {
+  if (grid < 1 || iters < 1 || !out_dev)
+    return mlxr::set_error(MLXR_E_INVALID, "mlxr_bench_mfma_peak: grid, iters >= 1 and an output buffer");
+  mlxr::mfma_peak_kernel<<<dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream>>>((float*)out_dev, iters);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MLXR_OK : mlxr::set_error(MLXR_E_HIP, "mfma peak launch: %s", hipGetErrorString(e));
+}
 
 extern "C" int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const size_t* bytes, void* sink_dev,
                                       int grid, void* stream) {
