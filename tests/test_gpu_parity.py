@@ -103,6 +103,8 @@ MFMA_CASES = [
     (Q6K, 128, 128, 1024), (Q6K, 200, 96, 512), (Q80, 128, 160, 1024), (Q80, 77, 64, 96),
     (Q40, 128, 256, 1024), (Q40, 33, 96, 96), (Q40, 8, 512, 2048), (Q41, 160, 128, 1056), (Q41, 64, 300, 4096),
     (Q41, 5, 64, 160),
+    # tile edges with N % 4 != 0 (the epilogue's scalar stores) and ragged M
+    (Q4K, 130, 250, 512), (Q6K, 300, 77, 256), (Q80, 200, 130, 1024),
     # one wavefront per workgroup (short K) with two M-blocks: every row must be stored
     (Q4K, 40, 64, 256), (Q6K, 64, 32, 512), (Q80, 33, 64, 64),
     (Q5K, 128, 256, 1024), (Q5K, 9, 96, 768), (Q5K, 300, 200, 2048),

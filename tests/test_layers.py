@@ -167,6 +167,28 @@ def test_q_gemm_swiglu_matches_oracle(cuda, qt, M):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M,N", [(130, 300), (257, 258), (300, 130)])
+def test_q_gemm_swiglu_ragged_tiles(cuda, M, N):
+    """The fused tiled kernel where the tile edges cut rows and columns: N not a multiple of
+    the 128-column SwiGLU tile, N % 4 != 0 (scalar stores), M not a multiple of 32, split
+    and unsplit, bf16 and fp32 outputs."""
+    import torch
+    qt, K = mx.QuantType.Q4_K, 1024
+    wg, wu = mx.synth_gguf(qt, N, K, 81), mx.synth_gguf(qt, N, K, 82)
+    pg = mx.pack_weights(wg, N, K, qt, device=cuda)
+    pu = mx.pack_weights(wu, N, K, qt, device=cuda)
+    x, xf = _act(torch, (M, K), 83 + M, cuda)
+    g = orc.gemm_f64(int(qt), M, N, K, wg, xf, w_to_bf16=True).astype(np.float64)
+    u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=True).astype(np.float64)
+    ref = _swiglu64(g, u)
+    for odt in (torch.bfloat16, torch.float32):
+        for ws in (True, False):
+            h = mx.q_gemm_swiglu(x, pg, pu, out_dtype=odt, workspace=ws)
+            assert h.shape == (M, N)
+            assert orc.rel_err(h.float().cpu().numpy(), ref) <= TOL, (odt, ws)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("M", [512, 2048])
 def test_q_gemm_swiglu_prefill_sizes(cuda, M):
     """The fused tiled kernel at prefill sizes (Llama-3-8B gate/up, K = 4096, N = 14336 cut
