@@ -618,6 +618,12 @@ def run_c5(cx, args):
                          "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                          "max_rel_err": err}
         del graphs
+        if M == 1:
+            # ceiling: the same five launches as pure streaming reads of the same packed weights
+            groups = (("q", "k"), ("v",), ("o",), ("gate", "up"), ("down",))
+            rms = stream_read_ms(cx, args, [[W[n] for n in g] for W in copies for g in groups]) / len(copies)
+            res["M=1"]["stream_read_ms_per_layer"] = round(rms, 4)
+            res["M=1"]["vs_stream_read"] = round(rms / ms, 4)
         if M > 4:
             # beside it: the seven projections as seven separate calls
             def sep_fn(W):
