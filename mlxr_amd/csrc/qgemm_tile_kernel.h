@@ -26,9 +26,11 @@
 //    for registers); the dequant of step k+1 is spread over the MFMAs of step k, a few
 //    VALU ops per MFMA.
 //  * One barrier per step, half way through it: the next stage is then complete and the
-//    previous one free for the DMA three steps ahead.
+//    previous one free for the DMA three steps ahead, which goes out over the second half
+//    of the step (one instruction every third MFMA slot).
 //  * The MFMAs take the weights as the first operand, so each lane's accumulators hold
-//    four consecutive output columns: the epilogue stores 8 or 16 bytes per access.
+//    four consecutive output columns; the epilogue turns each 32 x 64 block around through
+//    LDS and stores whole row segments (8 or 16 bytes per lane).
 //
 // The dequantized values are the exact GGUF fp32 weights rounded to nearest-even bf16
 // (fp16 for fp16 activations, which use the fp16 MFMA), from the routines of
@@ -97,11 +99,7 @@ struct TileParams {
 // reads take rows r .. r+15 of one chunk column per 16-lane phase; with 128-byte rows
 // and 64 four-byte banks, row r lands in bank group 8(r & 1) + (c ^ swz(r)), so swz must
 // be a bijection on the eight even and on the eight odd rows of an aligned group of 16.
-#ifndef MLXR_SWZ_LEGACY
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
-#else
-__device__ __forceinline__ int swz(int r) { return r & 7; }
-#endif
 
 template <int XT>
 __device__ __forceinline__ f32x16_t mfma(const uint4& a, const uint4& b, const f32x16_t& c) {
