@@ -322,7 +322,8 @@ def run_headline(cx, args, out):
             "us_per_layer": round(1e3 * ms_model / len(copies), 3),
             "stream_read_ceiling": {
                 "what": "pure non-temporal streaming read of the same packed weight buffers in the same "
-                        "launch structure (4 launches per layer, 128 per step, one graph), nothing computed",
+                        "launch structure (4 launches per layer, 128 per step, one graph), nothing computed; "
+                        "2048 workgroups per launch, the best grid of a 256-16384 sweep",
                 "ms_per_step": round(ms_ceiling, 5),
                 "GBps": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9, 1),
                 "frac_hbm": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
