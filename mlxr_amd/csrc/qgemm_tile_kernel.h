@@ -315,6 +315,9 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   __syncthreads();
   // Activation fragments stream through a ring of four registers, three ahead, across
   // step boundaries.
+  // reads from the next step's stage (fragments NF-3 .. NF-1 of a step) must come after
+  // the mid-step barrier (MFMA slot NSLOT/2 - 1, fragment NF/2 - 1) that completes it
+  static_assert(NF - 3 > NF / 2 - 1, "fragment lookahead overtakes the stage barrier");
   uint4 ring[4];
   ring[0] = read_a(0, 0);
   ring[1] = read_a(0, 1);
