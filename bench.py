@@ -118,6 +118,55 @@ class Ctx:
         return g
 
 
+_BLIB = None
+
+
+def blib():
+    """libmlxr_bench.so: the benchmark's measurement probes (stream read, MFMA rate), built
+    beside the matmul library but not part of it."""
+    global _BLIB
+    if _BLIB is None:
+        import ctypes
+        path = os.path.join(ROOT, "mlxr_amd", "lib", "libmlxr_bench.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build with `python -m mlxr_amd.build`")
+        lb = ctypes.CDLL(path)
+        lb.mlxr_bench_stream_read.restype = ctypes.c_int
+        lb.mlxr_bench_stream_read.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_int, ctypes.c_void_p]
+        lb.mlxr_bench_mfma_peak.restype = ctypes.c_int
+        lb.mlxr_bench_mfma_peak.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        _BLIB = lb
+    return _BLIB
+
+
+def bcheck(rc):
+    if rc != 0:
+        raise RuntimeError(f"bench probe launch failed (status {rc})")
+
+
+def pack_arena(cx, specs, seed0, ncopies):
+    """Like pack_copies, but each copy of the layer is one allocation holding its weights in
+    spec order (256-byte aligned), as a model loader lays a layer out: the weights of one
+    launch are then one contiguous byte range.  Returns (gguf, copies, arenas, ranges) with
+    ranges[name] = (offset, packed bytes)."""
+    mx, torch = cx.mx, cx.torch
+    gguf = {name: mx.synth_gguf(qt, N, K, seed0 + 16 * i) for i, (name, N, K, qt) in enumerate(specs)}
+    ranges, off = {}, 0
+    for name, N, K, qt in specs:
+        sz = mx.packed_size(qt, N, K)
+        ranges[name] = (off, sz)
+        off = (off + sz + 255) // 256 * 256
+    copies, arenas = [], []
+    for _ in range(ncopies):
+        arena = torch.empty(off, dtype=torch.uint8, device=cx.dev)
+        copies.append({name: mx.pack_weights(gguf[name], N, K, qt, out=arena[ranges[name][0]:sum(ranges[name])])
+                       for name, N, K, qt in specs})
+        arenas.append(arena)
+    torch.cuda.synchronize()
+    return gguf, copies, arenas, ranges
+
+
 def pack_copies(cx, specs, seed0, min_copies=2):
     """specs: [(name, N, K, qtype)] -> (gguf dict, list of {name: PackedWeight})."""
     mx = cx.mx
@@ -183,12 +232,12 @@ def stream_read_ms(cx, args, launches):
         sizes = (ctypes.c_size_t * len(pws))(*[pw.nbytes for pw in pws])
         grid = int(min(-(-sum(pw.nbytes for pw in pws) // 4096), 2048))
         calls.append((len(pws), ptrs, sizes, grid))
-    lib = mx.qgemm.lib()
+    lib = blib()
 
     def seq():
         st = mx.qgemm._stream_ptr(None)
         for n, ptrs, sizes, grid in calls:
-            mx.qgemm._check(lib.mlxr_bench_stream_read(n, ptrs, sizes, sink.data_ptr(), grid, st))
+            bcheck(lib.mlxr_bench_stream_read(n, ptrs, sizes, sink.data_ptr(), grid, st))
 
     g = cx.graph(seq)
     for _ in range(args.warmup):
@@ -196,6 +245,28 @@ def stream_read_ms(cx, args, launches):
     torch.cuda.synchronize()
     ms = cx.event_ms(lambda r: g.replay(), args.steps)
     del g
+    return ms
+
+
+def copy_ms(cx, args, ranges):
+    """Graph-replayed time of a sequence of device-to-device copies (hipMemcpyAsync through
+    torch's copy_), one per launch: ranges = [(arena, offset, bytes)], each copied into one
+    scratch buffer.  Milliseconds per replay of the whole sequence.  An independent reader
+    beside the stream-read probe: the runtime's own copy of the same bytes in the same
+    launch structure (its bytes read are the weights, counted once)."""
+    torch = cx.torch
+    dst = torch.empty(max(n for _, _, n in ranges), dtype=torch.uint8, device=cx.dev)
+
+    def seq():
+        for a, o, n in ranges:
+            dst[:n].copy_(a[o:o + n])
+
+    g = cx.graph(seq)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = cx.event_ms(lambda r: g.replay(), args.steps)
+    del g, dst
     return ms
 
 
@@ -213,9 +284,9 @@ def cpu_model():
 def run_headline(cx, args, out):
     mx, torch = cx.mx, cx.torch
     specs = [(n, N, K, Q4K) for n, N, K in LLAMA3_8B]
-    # one packed copy per layer of the model: the timed step streams 32 distinct layers
-    gguf, copies, layer = pack_copies(cx, specs, SEED_BASE + 1, min_copies=LLAMA3_8B_LAYERS)
-    copies = copies[:LLAMA3_8B_LAYERS]
+    # one packed copy per layer of the model (one allocation per layer, the weights in
+    # projection order): the timed step streams 32 distinct layers
+    gguf, copies, arenas, wr = pack_arena(cx, specs, SEED_BASE + 1, LLAMA3_8B_LAYERS)
     x = {4096: cx.act(1, 4096, mx.BF16, SEED_BASE + 1001), 14336: cx.act(1, 14336, mx.BF16, SEED_BASE + 1002)}
     ys = {n: torch.empty((1, N), dtype=torch.bfloat16, device=cx.dev) for n, N, K in LLAMA3_8B}
     dims = {n: (N, K) for n, N, K in LLAMA3_8B}
@@ -223,6 +294,7 @@ def run_headline(cx, args, out):
     step_bytes = sum(alg.values())
     # one decoder layer = 4 launches: the projections of one input run as one grouped launch
     LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
+    span = {ln: (wr[names[0]][0], sum(wr[names[-1]]) - wr[names[0]][0]) for ln, names in LAUNCHES}
 
     def launch(W, names):
         K = dims[names[0]][1]
@@ -258,12 +330,10 @@ def run_headline(cx, args, out):
         torch.cuda.synchronize()
         warm_us[lname] = 1e3 * cx.event_ms(lambda r: g.replay(), max(args.steps // 2, 5)) / R
         del g
-    avg_us = float(np.mean(list(kern_us.values())))
-    achieved = (step_bytes / len(LAUNCHES)) / (avg_us * 1e-6) / 1e9
 
     # the timed step: one token through the 32 layers' projections (4 launches per layer,
     # 128 in all, each layer its own weights), captured as one hipGraph as a decode engine
-    # captures its model
+    # captures its model; HIP events on the launch stream bracket the timed replays
     model = cx.graph(lambda: [step(W) for W in copies])
     for _ in range(args.warmup):
         model.replay()
@@ -271,12 +341,17 @@ def run_headline(cx, args, out):
     ms_model = cx.event_ms(lambda r: model.replay(), args.steps)
     del model
     # the same step's launch structure with a pure streaming read of the same packed weight
-    # buffers in place of each GEMV launch (mlxr_bench_stream_read): the HBM ceiling of
+    # buffers in place of each GEMV launch (libmlxr_bench stream read): the HBM ceiling of
     # 4 launches per layer, 128 per step, in one graph
     ms_ceiling = stream_read_ms(cx, args, [[W[n] for n in names] for W in copies for _, names in LAUNCHES])
     # and per launch kind: R back-to-back reads of one kind's buffers (as kern_us above)
     read_us = {lname: 1e3 * stream_read_ms(cx, args, [[copies[r % len(copies)][n] for n in names] for r in range(R)]) / R
                for lname, names in LAUNCHES}
+    # an independent reader: the runtime's device-to-device copy of each launch's packed
+    # bytes (one contiguous range per launch), in the same 128-launch structure and per kind
+    ms_copy = copy_ms(cx, args, [(A, span[ln][0], span[ln][1]) for A in arenas for ln, _ in LAUNCHES])
+    copy_us = {ln: 1e3 * copy_ms(cx, args, [(arenas[r % len(arenas)], span[ln][0], span[ln][1]) for r in range(R)]) / R
+               for ln, _ in LAUNCHES}
     # one layer per graph (a graph launch per 4 kernels), for comparison
     graphs = [cx.graph(lambda W=W: step(W)) for W in copies[:8]]
     for c in range(args.warmup):
@@ -298,24 +373,53 @@ def run_headline(cx, args, out):
         torch.cuda.synchronize()
         grouped_ok = all(torch.equal(y_g[n], ys[n]) for n in ys)
 
+    # the decoder's MLP block as it runs in a layer: mlxr_qgemm_mlp_ex (gate/up and the
+    # gating in one launch, then down over the real h), two launches; and its one-launch
+    # mode.  Same weights and launch count per layer as the step above minus one.
+    ws_mlp = mx.MlpWorkspace(cx.dev)
+    y_mlp = torch.empty((1, 4096), dtype=torch.bfloat16, device=cx.dev)
+    mlp_ms = {}
+    for mname, mode in (("chain", mx.qgemm.MLP_CHAIN), ("one_launch", mx.qgemm.MLP_ONE_LAUNCH)):
+        def dstep(W, mode=mode):
+            launch(W, ("q", "k", "v"))
+            launch(W, ("o",))
+            mx.q_gemm_mlp(x[4096], W["gate"], W["up"], W["down"], ws_mlp, out=y_mlp, mode=mode)
+        g = cx.graph(lambda: [dstep(W) for W in copies])
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        mlp_ms[mname] = cx.event_ms(lambda r: g.replay(), args.steps)
+        del g
+    ws_mlp.status()
+
     # accuracy of one layer of the step (as the graph ran it): every output
     step(copies[0])
     torch.cuda.synchronize()
     head_err = worst([rel_errs(cx, copies[0][n], x[dims[n][1]], ys[n], False) for n, _, _ in LLAMA3_8B])
 
-    traffic = None
+    traffic = traffic_src = None
     if os.path.exists(TRAFFIC_FILE):
         for line in open(TRAFFIC_FILE):
             if line.startswith("traffic_bytes_per_launch:"):
                 traffic = float(line.split(":")[1])
+            if line.startswith("measured:"):
+                traffic_src = line.split(":", 1)[1].strip()
 
+    nlaunch = len(copies) * len(LAUNCHES)
+    step_gbs = len(copies) * step_bytes / (ms_model * 1e-3) / 1e9
     out.update({
-        "value": round(len(copies) * step_bytes / (ms_model * 1e-3) / 1e9, 1),
+        "value": round(step_gbs, 1),
         "ms_per_step": round(ms_model, 5),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qgemv_lds_kernel<Q4_K,bf16,M=1> (4 launches per step: qkv, o, gate_up, down)",
-                     "kernel_avg_us": round(avg_us, 3), "alg_bytes_per_launch": round(step_bytes / len(LAUNCHES))},
+        "roofline": {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "qgemv_lds_kernel<Q4_K,bf16,M=1>: every launch of the step (128: qkv, o, gate_up, "
+                               "down per layer)",
+                     "achieved_from": "algorithmic bytes per step / ms_per_step (HIP events on the launch stream "
+                                      "over the timed replays); per launch: alg_bytes_per_launch / us_per_launch",
+                     "alg_bytes_per_launch": round(step_bytes / len(LAUNCHES)),
+                     "us_per_launch_in_step": round(1e3 * ms_model / nlaunch, 3),
+                     "traffic_from": "profiles/q4k_gemv_llama3_8b_m1_traffic.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
+                                     "mean bytes per launch; measured %s), not measured in this run" % traffic_src},
         "headline_detail": {
             "max_rel_err": head_err,
             "layers_per_step": len(copies), "layer_bytes": step_bytes,
@@ -328,22 +432,37 @@ def run_headline(cx, args, out):
                 "GBps": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9, 1),
                 "frac_hbm": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "gemv_step_vs_ceiling": round(ms_ceiling / ms_model, 4)},
+            "copy_ceiling": {
+                "what": "the runtime's device-to-device copy (hipMemcpyAsync via torch copy_) of each launch's "
+                        "packed weight bytes (one contiguous range per launch) in the same 128-launch graph; "
+                        "GBps counts the bytes read once (the copy also writes them)",
+                "ms_per_step": round(ms_copy, 5),
+                "GBps": round(len(copies) * step_bytes / (ms_copy * 1e-3) / 1e9, 1),
+                "frac_hbm": round(len(copies) * step_bytes / (ms_copy * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "gemv_step_vs_copy": round(ms_copy / ms_model, 4)},
             "one_layer_graph_ms": round(ms_graph, 5),
             "one_layer_graph_GBps": round(step_bytes / (ms_graph * 1e-3) / 1e9, 1),
             "launches": {ln: {"us": round(kern_us[ln], 3), "bytes": lbytes[ln],
                               "GBps": round(lbytes[ln] / (kern_us[ln] * 1e-6) / 1e9, 1),
                               "frac_hbm": round(lbytes[ln] / (kern_us[ln] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                               "stream_read_us": round(read_us[ln], 3),
-                              "vs_stream_read": round(read_us[ln] / kern_us[ln], 4)}
+                              "vs_stream_read": round(read_us[ln] / kern_us[ln], 4),
+                              "copy_us": round(copy_us[ln], 3),
+                              "vs_copy": round(copy_us[ln] / kern_us[ln], 4)}
                          for ln, _ in LAUNCHES},
             "warm_launches_infinity_cache": {ln: {"us": round(warm_us[ln], 3),
                                                   "GBps": round(lbytes[ln] / (warm_us[ln] * 1e-6) / 1e9, 1)}
                                              for ln, _ in LAUNCHES},
+            "decoder_mlp_step": {
+                "what": "the same 32 layers with the MLP block as a decoder runs it (mlxr_qgemm_mlp_ex: down over "
+                        "the real h); GBps over the same layer bytes",
+                **{k: {"ms_per_step": round(v, 5), "GBps": round(len(copies) * step_bytes / (v * 1e-3) / 1e9, 1),
+                       "launches_per_layer": 4 if k == "chain" else 3} for k, v in mlp_ms.items()}},
             "dropin_7_calls_graph_ms": ms_graph7 and round(ms_graph7, 5),
             "dropin_7_calls_graph_GBps": ms_graph7 and round(step_bytes / (ms_graph7 * 1e-3) / 1e9, 1),
             "dropin_7_calls_eager_ms": ms_eager7 and round(ms_eager7, 5),
             "grouped_equals_separate_calls": grouped_ok,
-            "weight_copies_rotated": len(copies), "rotated_MB": round(len(copies) * layer / 1e6, 1)},
+            "weight_copies_rotated": len(copies), "rotated_MB": round(sum(a.numel() for a in arenas) / 1e6, 1)},
     })
 
     if not args.no_cpu:
@@ -393,7 +512,7 @@ def run_headline(cx, args, out):
             "kind": "port", "dequant_s": round(dq, 4), "matmul_s": round(mm, 4),
             "sample": "one layer of the headline step: oracle fp32 dequant (OpenMP) + host BLAS fp32 GEMV "
                       "(torch.matmul), all cores of the process's CPU share; median of 5 runs"}
-    del graphs, graphs7, copies
+    del graphs, graphs7, copies, arenas
     torch.cuda.empty_cache()
 
 
@@ -502,9 +621,8 @@ def run_c4(cx, args):
     cus = torch.cuda.get_device_properties(cx.dev).multi_processor_count
     iters = 1024
     out = torch.empty(cus * 256, dtype=torch.float32, device=cx.dev)
-    lib = mx.qgemm.lib()
-    fn = lambda r: mx.qgemm._check(lib.mlxr_bench_mfma_peak(cus, iters, out.data_ptr(),
-                                                             torch.cuda.current_stream().cuda_stream))
+    lib = blib()
+    fn = lambda r: bcheck(lib.mlxr_bench_mfma_peak(cus, iters, out.data_ptr(), torch.cuda.current_stream().cuda_stream))
     fn(0)
     us = 1e3 * cx.graph_ms(fn, 4)
     tf = cus * 4 * iters * 16 * 32768 / us / 1e6
@@ -677,6 +795,17 @@ def main():
             torch.cuda.empty_cache()
     if configs:
         out["configs"] = configs
+    c4 = configs.get("c4_q4k_prefill")
+    if c4:
+        # the metric's other half: the prefill GEMM at M = 2048 on the matrix cores
+        r = c4["M=2048"]
+        out["roofline_prefill"] = {
+            "bound": "mfma", "achieved": r["TFLOPs"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": r["frac_bf16_peak"], "traffic": None,
+            "kernel": "qgemm_tile_kernel<Q4_K> (tiled bf16 MFMA GEMM; the seven Llama-3-8B projections at M=2048 "
+                      "as seven graph-replayed calls)",
+            "layer_as_4_grouped_calls": r["layer_grouped_4_calls"],
+            "mfma_ceiling_TFLOPs": c4["mfma_ceiling"]["TFLOPs"]}
     if args.calib_copy_mb:
         # one device copy of a known size, for scaling the profiler's traffic counters
         nb = args.calib_copy_mb * 1000000

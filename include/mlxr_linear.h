@@ -61,17 +61,21 @@ class Linear {
   kernels::array weight_;  // Dtype::packed
   kernels::array bias_;
   kernels::array workspace_;  // split-K partial sums, grown on demand
+  void* ws_alloc_stream_ = nullptr;  // stream workspace_ was allocated (and is freed) on
+  void* ws_last_stream_ = nullptr;   // stream of its last use
 };
 
-// SwiGLU MLP (reference layers.cpp:383-414): down(swish(gate(x)) * up(x)).  gate, up and
-// the gating run as mlxr_qgemm_swiglu: one launch (plus a split-K reduce where it splits).
+// SwiGLU MLP (reference layers.cpp:383-414): down(swish(gate(x)) * up(x)).
 class MLP {
  public:
   MLP(int hidden_size, int intermediate_size);
   Linear& gate_proj() { return gate_; }
   Linear& up_proj() { return up_; }
   Linear& down_proj() { return down_; }
-  // x [..., hidden] -> [..., hidden]; h and the workspace are stream-ordered temporaries.
+  // x [..., hidden] -> [..., hidden] through mlxr_qgemm_mlp (at M = 1 the whole block is
+  // one launch); the output is a stream-ordered allocation on s and the workspace (sync
+  // words, h, split-K partials) is held by the layer, grown on demand.  One layer must not
+  // run this forward on two streams at once.
   kernels::array forward(const kernels::array& x, kernels::Stream s = {});
   // Same into the caller's y ([..., hidden], x's dtype) with the caller's h ([M,
   // intermediate] in x's dtype: swish(gate) * up) and workspace (workspace_size bytes;
@@ -84,6 +88,9 @@ class MLP {
  private:
   int hidden_, inter_;
   Linear gate_, up_, down_;
+  kernels::array workspace_;  // mlxr_qgemm_mlp workspace, grown (and initialised) on demand
+  void* ws_alloc_stream_ = nullptr;
+  void* ws_last_stream_ = nullptr;
 };
 
 }  // namespace graph

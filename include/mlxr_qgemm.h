@@ -19,8 +19,8 @@
  *   - Return value 0 = success, negative = error (MLXR_E_*); the message of the last
  *     error on the calling thread is returned by mlxr_qgemm_last_error().  No C++
  *     exception crosses this boundary.
- *   - Thread-safe: the library has no mutable global state besides the thread-local
- *     error string.
+ *   - Thread-safe: the library's only mutable global state is the thread-local error
+ *     string and the two test hooks' atomics.
  *   - Dequantized weights follow the GGUF block_q4_0 / block_q4_1 / block_q8_0 /
  *     block_q4_K / block_q5_K / block_q6_K definitions exactly (fp32 results are bit-exact to those
  *     formulas).
@@ -56,7 +56,8 @@ enum {
   MLXR_E_UNSUPPORTED = -2, /* quant type not implemented (reference: .mm:76,133,340) */
   MLXR_E_SHAPE = -3,       /* K not a multiple of the block size, group_size mismatch */
   MLXR_E_HIP = -4,         /* HIP runtime error (message has the HIP error string) */
-  MLXR_E_NOMEM = -5        /* device allocation failed (mlxr_qgemm_pack only) */
+  MLXR_E_NOMEM = -5,       /* device allocation failed (mlxr_qgemm_pack only) */
+  MLXR_E_TIMEOUT = -6      /* a fused MLP launch gave up its bounded wait (mlxr_qgemm_mlp_status) */
 };
 
 /* Execution path selector for mlxr_qgemm_run_ex. */
@@ -209,20 +210,50 @@ int mlxr_qgemm_swiglu(int qtype, int N, int K, const void* gate_packed, const vo
  * core/graph/layers.cpp:391-414, MLP::forward). */
 int mlxr_swiglu(const void* gate_dev, const void* up_dev, void* out_dev, size_t n, int dtype, void* stream);
 
-/* Benchmark probe, not part of the matmul path: one launch of `grid` workgroups that only
- * reads bytes[i] bytes (multiples of 16) of each of the nbuf (1-4) device buffers bufs[i],
- * with non-temporal loads, and writes nothing (sink_dev: 4 KiB of device memory it could
- * write).  bench.py times it over the headline step's weights in the step's launch
- * structure, as the HBM ceiling of that structure.  No counterpart in the reference. */
-int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const size_t* bytes, void* sink_dev, int grid,
-                           void* stream);
+/* SwiGLU MLP, y[M, hidden] = down( swish(x . gate^T) * (x . up^T) ), the whole MLP block
+ * of a decoder layer (reference core/graph/layers.cpp:391-414, MLP::forward;
+ * core/kernels/metal/swiglu_mlp_fused.metal:110-131 computes the same chain in one
+ * kernel).  gate and up are packed [inter, hidden] weights of qtype_gu, down a packed
+ * [hidden, inter] weight of qtype_down; x is [M, hidden] (BF16/F16), y [M, hidden].
+ * The gated intermediate h is kept in the activation type in the workspace.
+ *   MLXR_MLP_CHAIN (and MLXR_MLP_AUTO): mlxr_qgemm_swiglu into the workspace (one launch
+ *     for gate, up and the gating at every M), then the down projection.
+ *   MLXR_MLP_ONE_LAUNCH (M = 1, qtype_down == qtype_gu or MLXR_Q6_K; other calls run the
+ *     chain): one launch whose gate/up workgroups write h segment by segment and whose
+ *     down workgroups consume each segment once a device-scope counter says it is
+ *     complete (bounded waits).  Results equal the chain bit for bit.  Measured on
+ *     MI355X it is slower than the chain (Llama-3-8B: 28 us against 22 us), so AUTO does
+ *     not take it.
+ * The workspace (mlxr_qgemm_mlp_workspace_size bytes) starts with a 160 KiB sync region
+ * whose words must be zero before its first use: call mlxr_qgemm_mlp_workspace_init once
+ * after allocating it (a kernel, so it may also be captured).  Each launch leaves them
+ * zero again.  Calls that share a workspace must not overlap (same stream, or ordered
+ * streams).
+ * mlxr_qgemm_mlp_status synchronises `stream` and returns MLXR_E_TIMEOUT if a one-launch
+ * call on this workspace gave up its wait since the last status call (its y is invalid;
+ * only possible when the down workgroups wait 0.2 s, e.g. on a device shared with a
+ * kernel that never yields); it then re-initialises the sync region, so the next launch is
+ * exact.  No counterpart in the reference's operator. */
+enum { MLXR_MLP_AUTO = 0, MLXR_MLP_CHAIN = 1, MLXR_MLP_ONE_LAUNCH = 2 };
+#define MLXR_MLP_H_OFFSET 163840 /* byte offset of h ([M, inter], activation type) in the workspace */
+int mlxr_qgemm_mlp_workspace_size(int qtype_gu, int qtype_down, int hidden, int inter, int M, size_t* bytes);
+int mlxr_qgemm_mlp_workspace_init(void* workspace_dev, size_t workspace_bytes, void* stream);
+int mlxr_qgemm_mlp(int qtype_gu, int qtype_down, int hidden, int inter, const void* gate_packed,
+                   const void* up_packed, const void* down_packed, const void* x_dev, int x_dtype, void* y_dev,
+                   int y_dtype, int M, void* workspace_dev, size_t workspace_bytes, void* stream);
+int mlxr_qgemm_mlp_ex(int qtype_gu, int qtype_down, int hidden, int inter, const void* gate_packed,
+                      const void* up_packed, const void* down_packed, const void* x_dev, int x_dtype, void* y_dev,
+                      int y_dtype, int M, int mode, void* workspace_dev, size_t workspace_bytes, void* stream);
+int mlxr_qgemm_mlp_status(void* workspace_dev, void* stream);
 
-/* Benchmark probe: grid workgroups of four wavefronts (one per SIMD), each issuing
- * iters x 16 independent bf16 32x32x16 MFMAs from registers, no memory traffic; writes
- * grid * 256 floats to out_dev.  Flops per launch = grid * 4 * iters * 16 * 32768.  bench.py
- * times it as the matrix-core rate the part sustains under full load (the prefill GEMMs'
- * ceiling).  No counterpart in the reference. */
-int mlxr_bench_mfma_peak(int grid, int iters, void* out_dev, void* stream);
+/* Test hooks (no counterpart in the reference; not for production callers).
+ * mlxr_qgemm_test_set_operand_limit: the largest operand the 32-bit-offset kernels take in
+ * one launch (default 2 GiB; 0 restores it), lowered by tests so small shapes reach the
+ * chunked and fallback launches.  mlxr_qgemm_test_set_mlp_spin_limit: the fused MLP's wait
+ * bound in ticks of the 100 MHz real-time counter (default 0.2 s; 0 restores it), lowered
+ * by tests to exercise the timeout path.  Both are process-wide (atomics). */
+int mlxr_qgemm_test_set_operand_limit(size_t bytes);
+int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks);
 
 /* Deterministic synthetic inputs with the shapes/distributions of the benchmark
  * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by

@@ -1,4 +1,5 @@
-// Measurement kernels for the benchmark (not part of the matmul path).
+// Measurement kernels for the benchmark, built into their own library (libmlxr_bench.so),
+// not into the matmul library: nothing on the matmul path calls them.
 //  - stream_read_kernel: a pure streaming read of up to four device buffers in one launch,
 //    the bytes a grouped GEMV launch reads, with nothing computed on them.  bench.py runs
 //    it over the headline step's packed weights in the step's launch structure (one launch
@@ -10,9 +11,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/mlxr_qgemm.h"
-#include "qgemm_device.h"
-#include "qgemm_internal.h"
+
+// Exported (bench.py binds them with ctypes; return 0, -1 for invalid arguments, -4 for a
+// HIP launch error):
+//   int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const size_t* bytes,
+//                              void* sink_dev, int grid, void* stream);
+//     one launch of `grid` workgroups that only reads bytes[i] (multiples of 16) of each
+//     of the nbuf (1-4) buffers with non-temporal loads; sink_dev: 4 KiB it could write.
+//   int mlxr_bench_mfma_peak(int grid, int iters, void* out_dev, void* stream);
+//     grid workgroups of four wavefronts, each iters x 16 independent bf16 32x32x16 MFMAs
+//     (flops = grid * 4 * iters * 16 * 32768); writes grid * 256 floats to out_dev.
 
 namespace mlxr {
 namespace {
@@ -89,24 +97,22 @@ __global__ __launch_bounds__(256, 1) void mfma_peak_kernel(float* out, int iters
 }  // namespace mlxr
 
 extern "C" int mlxr_bench_mfma_peak(int grid, int iters, void* out_dev, void* stream) {
-  if (grid < 1 || iters < 1 || !out_dev)
-    return mlxr::set_error(MLXR_E_INVALID, "mlxr_bench_mfma_peak: grid, iters >= 1 and an output buffer");
+  if (grid < 1 || iters < 1 || !out_dev) return -1;
   mlxr::mfma_peak_kernel<<<dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream>>>((float*)out_dev, iters);
   const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? MLXR_OK : mlxr::set_error(MLXR_E_HIP, "mfma peak launch: %s", hipGetErrorString(e));
+  return e == hipSuccess ? 0 : -4;
 }
 
 extern "C" int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const size_t* bytes, void* sink_dev,
                                       int grid, void* stream) {
-  if (nbuf < 1 || nbuf > 4 || !bufs || !bytes || !sink_dev || grid < 1)
-    return mlxr::set_error(MLXR_E_INVALID, "mlxr_bench_stream_read: 1-4 buffers, a sink and a grid");
+  if (nbuf < 1 || nbuf > 4 || !bufs || !bytes || !sink_dev || grid < 1) return -1;
   mlxr::ReadParams rp;
   rp.total = 0;
   rp.nbuf = nbuf;
   rp.sink = (uint32_t*)sink_dev;
   for (int i = 0; i < 4; ++i) {
     const int k = i < nbuf ? i : 0;
-    if (!bufs[k] || (bytes[k] & 15)) return mlxr::set_error(MLXR_E_INVALID, "buffers must be 16-byte multiples");
+    if (!bufs[k] || (bytes[k] & 15)) return -1;
     rp.p[i] = (const uint8_t*)bufs[k];
     rp.n16[i] = i < nbuf ? bytes[k] / 16 : 0;
     rp.start[i] = rp.total;
@@ -114,5 +120,5 @@ extern "C" int mlxr_bench_stream_read(int nbuf, const void* const* bufs, const s
   }
   mlxr::stream_read_kernel<<<dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream>>>(rp);
   const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? MLXR_OK : mlxr::set_error(MLXR_E_HIP, "stream read launch: %s", hipGetErrorString(e));
+  return e == hipSuccess ? 0 : -4;
 }

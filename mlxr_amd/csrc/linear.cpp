@@ -28,6 +28,32 @@ int dt_code(kernels::Dtype d) {
   }
 }
 
+// Grows a layer-held stream-ordered workspace to `need` bytes for a use on s (returns
+// whether it was reallocated).  The old buffer is freed (hipFreeAsync) on the stream that
+// allocated it; when its last use was on another stream, that stream's work is made to
+// precede the free first, so the memory is not handed out again while a kernel of that
+// last use may still write into it.
+bool grow_workspace(kernels::array& ws, void*& alloc_stream, void*& last_stream, size_t need, kernels::Stream s) {
+  bool fresh = false;
+  if (need > ws.nbytes()) {
+    if (ws.nbytes() && last_stream != alloc_stream) {
+      hipEvent_t ev;
+      hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (e == hipSuccess) {
+        e = hipEventRecord(ev, (hipStream_t)last_stream);
+        if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)alloc_stream, ev, 0);
+        (void)hipEventDestroy(ev);
+      }
+      if (e != hipSuccess) throw std::runtime_error(std::string("layer workspace release: ") + hipGetErrorString(e));
+    }
+    ws = kernels::array({(int)need}, kernels::Dtype::uint8, s);
+    alloc_stream = s.hip_stream;
+    fresh = true;
+  }
+  last_stream = s.hip_stream;
+  return fresh;
+}
+
 }  // namespace
 
 Linear::Linear(int in_features, int out_features, bool bias)
@@ -104,8 +130,7 @@ kernels::array Linear::forward(const kernels::array& x, kernels::Stream s) {
   if (M > 0) {
     size_t ws = workspace_size((int)M);
     if (ws > 0x7fffffffu) ws = 0;  // beyond one array: run unsplit
-    // grown on demand; the old workspace is released in stream order after queued work
-    if (ws > workspace_.nbytes()) workspace_ = kernels::array({(int)ws}, kernels::Dtype::uint8, s);
+    grow_workspace(workspace_, ws_alloc_stream_, ws_last_stream_, ws, s);
     run(x, (int)M, y, workspace_.nbytes() ? workspace_.data<void>() : nullptr, workspace_.nbytes(), s);
   }
   return y;
@@ -150,16 +175,24 @@ void MLP::forward(const kernels::array& x, kernels::array& y, kernels::array& h,
 
 kernels::array MLP::forward(const kernels::array& x, kernels::Stream s) {
   const long M = rows_of(x, hidden_, "hidden_size");
-  std::vector<int> hshape = x.shape();
-  hshape.back() = inter_;
-  kernels::array h(hshape, x.dtype(), s);
   kernels::array y(x.shape(), x.dtype(), s);
-  size_t ws = M > 0 ? workspace_size((int)M, x.dtype()) : 0;
-  if (ws > 0x7fffffffu) throw std::runtime_error("MLP: workspace of 2 GiB or more");
-  kernels::array w;
-  if (ws) w = kernels::array({(int)ws}, kernels::Dtype::uint8, s);
-  forward(x, y, h, ws ? w.data<void>() : nullptr, ws, s);
-  // h and w are released in stream order (hipFreeAsync) after the queued kernels
+  if (M == 0) return y;
+  if (gate_.weight_.dtype() != kernels::Dtype::packed || up_.weight_.dtype() != kernels::Dtype::packed ||
+      down_.weight_.dtype() != kernels::Dtype::packed)
+    throw std::runtime_error("MLP: weights not loaded");
+  const int qt = (int)gate_.weight_.quant_type(), qd = (int)down_.weight_.quant_type();
+  if (qt != (int)up_.weight_.quant_type()) throw std::runtime_error("MLP: gate and up must share a quant type");
+  // the whole block through mlxr_qgemm_mlp: one launch at M = 1, else gate/up/gating and
+  // down; its workspace (sync words, h, split-K partials) is held by the layer
+  size_t need = 0;
+  check(mlxr_qgemm_mlp_workspace_size(qt, qd, hidden_, inter_, (int)M, &need));
+  if (need > 0x7fffffffu) throw std::runtime_error("MLP: workspace of 2 GiB or more");
+  if (grow_workspace(workspace_, ws_alloc_stream_, ws_last_stream_, need, s))
+    check(mlxr_qgemm_mlp_workspace_init(workspace_.data<void>(), workspace_.nbytes(), s.hip_stream));
+  const int dt = dt_code(x.dtype());
+  check(mlxr_qgemm_mlp(qt, qd, hidden_, inter_, gate_.weight_.data<void>(), up_.weight_.data<void>(),
+                       down_.weight_.data<void>(), x.data<void>(), dt, y.data<void>(), dt, (int)M,
+                       workspace_.data<void>(), workspace_.nbytes(), s.hip_stream));
   return y;
 }
 

@@ -9,6 +9,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <string>
 #include <vector>
 
@@ -42,12 +43,12 @@ int fail(int code, const char* fmt, ...) {
 
 namespace mlxr {
 
-size_t operand_limit() {
-  // test hook only (documented in qgemm_internal.h); read per call so a test can set it
-  const char* e = getenv("MLXR_MFMA_CHUNK_BYTES");
-  const long long v = e ? atoll(e) : 0;
-  return v > 0 ? std::min((size_t)1 << 31, (size_t)v) : (size_t)1 << 31;
-}
+namespace {
+// 2 GiB unless a test lowered it (mlxr_qgemm_test_set_operand_limit)
+std::atomic<size_t> g_operand_limit{(size_t)1 << 31};
+}  // namespace
+
+size_t operand_limit() { return g_operand_limit.load(std::memory_order_relaxed); }
 
 int set_error(int code, const char* fmt, ...) {
   char buf[512];
@@ -462,6 +463,151 @@ int mlxr_qgemm_run(int qtype, int N, int K, int group_size, const void* packed_d
                    void* stream) {
   return mlxr_qgemm_run_ex(qtype, N, K, group_size, packed_dev, x_dev, x_dtype, bias_dev, bias_dtype, y_dev,
                            y_dtype, M, MLXR_PATH_AUTO, stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ fused SwiGLU MLP
+
+namespace {
+
+constexpr size_t kMlpSyncBytes = (size_t)mlxr::kMlpSyncWords * 4;
+static_assert(kMlpSyncBytes == MLXR_MLP_H_OFFSET, "h follows the sync region");
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Validates the MLP's shapes; fills the layouts.
+int mlp_shapes(int qgu, int qd, int H, int I, int M, mlxr::MlpArgs* a) {
+  int rc = check_type_shape(qgu, I, H, &a->gate);
+  if (rc) return rc;
+  rc = check_type_shape(qd, H, I, &a->down);
+  if (rc) return rc;
+  if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
+  a->up = a->gate;
+  a->qtd = qd;
+  a->M = M;
+  a->H = H;
+  a->I = I;
+  return MLXR_OK;
+}
+
+// Workspace past the sync words and h: split-K partials of the unfused launches.
+int mlp_rest_bytes(int qgu, int qd, int H, int I, int M, size_t* bytes) {
+  size_t a = 0, b = 0;
+  int rc = mlxr_qgemm_swiglu_workspace_size(qgu, I, H, M, MLXR_BF16, &a);
+  if (rc) return rc;
+  rc = mlxr_qgemm_workspace_size(qd, H, I, M, &b);
+  if (rc) return rc;
+  *bytes = std::max(a, b);
+  return MLXR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlxr_qgemm_mlp_workspace_size(int qtype_gu, int qtype_down, int hidden, int inter, int M, size_t* bytes) {
+  mlxr::MlpArgs a;
+  int rc = mlp_shapes(qtype_gu, qtype_down, hidden, inter, M, &a);
+  if (rc) return rc;
+  if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
+  size_t rest = 0;
+  rc = mlp_rest_bytes(qtype_gu, qtype_down, hidden, inter, M, &rest);
+  if (rc) return rc;
+  *bytes = kMlpSyncBytes + align256((size_t)M * (size_t)inter * 2) + rest;
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_mlp_workspace_init(void* workspace_dev, size_t workspace_bytes, void* stream) {
+  if (!workspace_dev || workspace_bytes < kMlpSyncBytes)
+    return fail(MLXR_E_INVALID, "MLP workspace must be at least %zu bytes (got %zu)", kMlpSyncBytes,
+                workspace_dev ? workspace_bytes : (size_t)0);
+  const hipError_t e = mlxr::launch_mlp_sync_zero((unsigned*)workspace_dev, (hipStream_t)stream);
+  return e != hipSuccess ? hip_fail(e, "mlp workspace init") : MLXR_OK;
+}
+
+int mlxr_qgemm_mlp(int qtype_gu, int qtype_down, int hidden, int inter, const void* gate_packed,
+                   const void* up_packed, const void* down_packed, const void* x_dev, int x_dtype, void* y_dev,
+                   int y_dtype, int M, void* workspace_dev, size_t workspace_bytes, void* stream) {
+  return mlxr_qgemm_mlp_ex(qtype_gu, qtype_down, hidden, inter, gate_packed, up_packed, down_packed, x_dev, x_dtype,
+                           y_dev, y_dtype, M, MLXR_MLP_AUTO, workspace_dev, workspace_bytes, stream);
+}
+
+int mlxr_qgemm_mlp_ex(int qtype_gu, int qtype_down, int hidden, int inter, const void* gate_packed,
+                      const void* up_packed, const void* down_packed, const void* x_dev, int x_dtype, void* y_dev,
+                      int y_dtype, int M, int mode, void* workspace_dev, size_t workspace_bytes, void* stream) {
+  if (mode != MLXR_MLP_AUTO && mode != MLXR_MLP_CHAIN && mode != MLXR_MLP_ONE_LAUNCH)
+    return fail(MLXR_E_INVALID, "invalid MLP mode %d", mode);
+  mlxr::MlpArgs a;
+  int rc = mlp_shapes(qtype_gu, qtype_down, hidden, inter, M, &a);
+  if (rc) return rc;
+  if (x_dtype != MLXR_BF16 && x_dtype != MLXR_F16)
+    return fail(MLXR_E_INVALID, "activation dtype must be BF16 or F16 (got %d)", x_dtype);
+  if (!valid_dtype(y_dtype)) return fail(MLXR_E_INVALID, "invalid output dtype %d", y_dtype);
+  if (M == 0) return MLXR_OK;
+  if (!gate_packed || !up_packed || !down_packed || !x_dev || !y_dev)
+    return fail(MLXR_E_INVALID, "null buffer");
+  size_t need = 0;
+  rc = mlxr_qgemm_mlp_workspace_size(qtype_gu, qtype_down, hidden, inter, M, &need);
+  if (rc) return rc;
+  if (!workspace_dev || workspace_bytes < need)
+    return fail(MLXR_E_INVALID, "the MLP at M=%d needs a workspace of %zu bytes (got %zu)", M, need,
+                workspace_dev ? workspace_bytes : (size_t)0);
+  uint8_t* ws = (uint8_t*)workspace_dev;
+  a.gate_packed = gate_packed;
+  a.up_packed = up_packed;
+  a.down_packed = down_packed;
+  a.x = x_dev;
+  a.x_dtype = x_dtype;
+  a.sync = (unsigned*)ws;
+  a.h = ws + kMlpSyncBytes;
+  a.y = y_dev;
+  a.y_dtype = y_dtype;
+  hipStream_t s = (hipStream_t)stream;
+  // the one-launch kernel only when asked for: on MI355X it is slower than the two launches
+  // (Llama-3-8B at M = 1: 28 us against 22 us)
+  if (mode == MLXR_MLP_ONE_LAUNCH && mlxr::mlp_fused_ok(a)) {
+    const hipError_t e = mlxr::launch_mlp_fused(a, s);
+    return e != hipSuccess ? hip_fail(e, "mlp launch") : MLXR_OK;
+  }
+  // two launches: gate/up with the gating, then down over h
+  const size_t hb = align256((size_t)M * (size_t)inter * 2);
+  void* rest = ws + kMlpSyncBytes + hb;
+  const size_t rest_bytes = workspace_bytes - kMlpSyncBytes - hb;
+  rc = mlxr_qgemm_swiglu(qtype_gu, inter, hidden, gate_packed, up_packed, x_dev, x_dtype, a.h, x_dtype, M, rest,
+                         rest_bytes, stream);
+  if (rc) return rc;
+  return mlxr_qgemm_run_ws(qtype_down, hidden, inter, 0, down_packed, a.h, x_dtype, nullptr, MLXR_F32, y_dev,
+                           y_dtype, M, MLXR_PATH_AUTO, rest, rest_bytes, stream);
+}
+
+int mlxr_qgemm_mlp_status(void* workspace_dev, void* stream) {
+  if (!workspace_dev) return fail(MLXR_E_INVALID, "null workspace");
+  unsigned flag = 0;
+  unsigned* f = (unsigned*)workspace_dev + mlxr::kMlpSlotWords * mlxr::kMlpErr;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = hipMemcpyAsync(&flag, f, sizeof(flag), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  // after a timeout the counters may be left mid-count: the whole sync region is zeroed
+  if (e == hipSuccess && flag) e = mlxr::launch_mlp_sync_zero((unsigned*)workspace_dev, s);
+  if (e == hipSuccess && flag) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "mlp status");
+  if (flag)
+    return fail(MLXR_E_TIMEOUT,
+                "a fused MLP launch on this workspace gave up waiting for its gate/up workgroups; its output is "
+                "invalid");
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks) {
+  mlxr::set_mlp_spin_limit(ticks ? ticks : 20000000u);
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_test_set_operand_limit(size_t bytes) {
+  const size_t full = (size_t)1 << 31;
+  mlxr::g_operand_limit.store(bytes ? std::min(bytes, full) : full, std::memory_order_relaxed);
+  return MLXR_OK;
 }
 
 }  // extern "C"

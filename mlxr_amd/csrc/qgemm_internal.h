@@ -63,8 +63,8 @@ hipError_t launch_mfma_grouped(const RunArgs* const* items, int n, void* ws, siz
 size_t mfma_grouped_workspace_bytes(const RunArgs* const* items, int n);
 
 // Largest operand (activations, weight plane) the 32-bit-offset kernels address in one
-// launch: 2 GiB.  Test hook: the environment variable MLXR_MFMA_CHUNK_BYTES lowers it (read
-// on each call), so the tests reach the chunked and fallback launches at small sizes.
+// launch: 2 GiB.  Test hook: mlxr_qgemm_test_set_operand_limit lowers it (an atomic), so the
+// tests reach the chunked and fallback launches at small sizes.
 size_t operand_limit();
 
 // Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.  With a.ws,
@@ -91,5 +91,39 @@ hipError_t launch_splitk_reduce_swiglu(const float* ws, size_t split_elems, int 
 // y = sum of S fp32 partial planes (split order) + bias, converted (qgemm_tile.hip).
 hipError_t launch_splitk_reduce(const float* ws, size_t split_elems, int S, const void* bias, int bias_dtype, void* y,
                                 int y_dtype, int M, int N, hipStream_t s);
+
+// Fused SwiGLU MLP (qgemm_mlp.hip): y = down(swish(x . gate^T) * (x . up^T)).
+// Sync region at the start of its workspace, one word per 256-byte slot: for each of up
+// to kMlpMaxSeg segments of h, kMlpSegSub arrival counters, their top counter and
+// kMlpGoCopies go flags; then kMlpDepartN departure counters, their top counter and the
+// error flag.
+constexpr int kMlpSlotWords = 64;
+constexpr int kMlpMaxSeg = 32, kMlpSegSub = 8, kMlpGoCopies = 8;
+constexpr int kMlpSegSlots = kMlpSegSub + 1 + kMlpGoCopies;
+constexpr int kMlpDepartSub = kMlpMaxSeg * kMlpSegSlots, kMlpDepartN = 32;
+constexpr int kMlpDepartTop = kMlpDepartSub + kMlpDepartN, kMlpErr = kMlpDepartTop + 1;
+constexpr int kMlpSlots = 640;  // kMlpErr + 1 rounded up
+static_assert(kMlpErr < kMlpSlots, "sync region");
+constexpr int kMlpSyncWords = kMlpSlots * kMlpSlotWords;  // 160 KiB
+struct MlpArgs {
+  PackedLayout gate, up, down;  // gate/up [I, H], down [H, I]
+  int qtd;                      // down's quant type (gate's, or Q6_K)
+  const void *gate_packed, *up_packed, *down_packed;
+  const void* x;  // [M, H]
+  int x_dtype;
+  void* h;  // [M, I] in the activation type (workspace)
+  void* y;  // [M, H]
+  int y_dtype;
+  unsigned* sync;  // kMlpSyncWords words, zero between calls
+  int M, H, I;
+};
+// Whether the one-launch kernel serves the call (M = 1, down of gate's type or Q6_K,
+// operands below 2 GiB, activations fit LDS, at most kMlpMaxSeg segments of h).
+bool mlp_fused_ok(const MlpArgs& a);
+hipError_t launch_mlp_fused(const MlpArgs& a, hipStream_t s);
+// Zeroes the sync words with a kernel (no memset node in a captured graph).
+hipError_t launch_mlp_sync_zero(unsigned* sync, hipStream_t s);
+// Bound of the down workgroups' wait, in ticks of the 100 MHz real-time counter.
+void set_mlp_spin_limit(uint32_t ticks);
 
 }  // namespace mlxr

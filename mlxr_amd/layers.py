@@ -83,27 +83,34 @@ class Linear:
 
 
 class MLP:
-    """down(swish(gate(x)) * up(x)); gate, up and the gating are one launch."""
+    """down(swish(gate(x)) * up(x)) through mlxr_qgemm_mlp: at M = 1 the whole block is one
+    launch; above, the fused gate/up/gating launch and the down projection.  The layer holds
+    the workspace (sync words, h, split-K partials)."""
 
     def __init__(self, hidden_size, intermediate_size):
         self.hidden_size, self.intermediate_size = hidden_size, intermediate_size
         self.gate_proj = Linear(hidden_size, intermediate_size)
         self.up_proj = Linear(hidden_size, intermediate_size)
         self.down_proj = Linear(intermediate_size, hidden_size)
+        self._ws = None
 
     def forward(self, x, stream=None):
         if x.dim() < 1 or x.shape[-1] != self.hidden_size:
             raise QGemmError(-3, "Input shape must be [..., hidden_size]")
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.hidden_size)
-        M = x2.shape[0]
-        gw, uw = self.gate_proj.weight, self.up_proj.weight
+        gw, uw, dw = self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight
+        if gw is None or uw is None or dw is None:
+            raise QGemmError(-1, "MLP: weights not loaded")
         if (gw.qtype, gw.N) == (uw.qtype, uw.N):
-            h = qgemm.q_gemm_swiglu(x2, gw, uw, stream=stream)  # one fused launch
+            if self._ws is None:
+                self._ws = qgemm.MlpWorkspace(x.device)
+            y = qgemm.q_gemm_mlp(x2, gw, uw, dw, self._ws, stream=stream)
         else:
             g = self.gate_proj.forward(x2, stream=stream)
             u = self.up_proj.forward(x2, stream=stream)
             h = swiglu(g, u, out=g, stream=stream)
-        return self.down_proj.forward(h, stream=stream).reshape(*lead, self.hidden_size)
+            y = self.down_proj.forward(h, stream=stream)
+        return y.reshape(*lead, self.hidden_size)
 
     __call__ = forward

@@ -17,6 +17,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libmlxr_qgemm.so")
 
 F32, F16, BF16 = 0, 1, 2
+MLP_AUTO, MLP_CHAIN, MLP_ONE_LAUNCH = 0, 1, 2
+MLP_H_OFFSET = 163840  # MLXR_MLP_H_OFFSET: byte offset of h in an MLP workspace
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
 
 
@@ -70,8 +72,6 @@ _SIGS = {
     "mlxr_qgemm_run_ex": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_workspace_size": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_size_t)]),
     "mlxr_qgemm_run_ws": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
-    "mlxr_bench_stream_read": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]),
-    "mlxr_bench_mfma_peak": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
     "mlxr_qgemm_run_noalloc": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p] * 2 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_swiglu_workspace_size": (ctypes.c_int, [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_size_t)]),
     "mlxr_qgemm_swiglu": (ctypes.c_int, [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
@@ -79,6 +79,13 @@ _SIGS = {
     "mlxr_qgemm_run_grouped": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "mlxr_qgemm_run_grouped_ws": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "mlxr_qgemm_grouped_workspace_size": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]),
+    "mlxr_qgemm_mlp_workspace_size": (ctypes.c_int, [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_size_t)]),
+    "mlxr_qgemm_mlp_workspace_init": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mlxr_qgemm_mlp": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mlxr_qgemm_mlp_ex": (ctypes.c_int, [ctypes.c_int] * 4 + [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "mlxr_qgemm_mlp_status": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "mlxr_qgemm_test_set_operand_limit": (ctypes.c_int, [ctypes.c_size_t]),
+    "mlxr_qgemm_test_set_mlp_spin_limit": (ctypes.c_int, [ctypes.c_uint]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
 }
@@ -192,20 +199,26 @@ class PackedWeight:
         return self.buf.numel()
 
 
-def pack_weights(gguf, N, K, qtype, device="cuda", stream=None):
+def pack_weights(gguf, N, K, qtype, device="cuda", stream=None, out=None):
     """One-time upload of GGUF blocks (numpy/CPU tensor/device tensor) to the packed layout.
 
     The packed buffer and any device staging copy are allocated on the stream the pack runs
     on (torch's stream-ordered allocator), so a staging copy freed on return is reused only
-    after the pack."""
+    after the pack.  ``out``: a contiguous uint8 device tensor of packed_size bytes to pack
+    into instead (e.g. a slice of one allocation that holds a whole layer)."""
     torch = _torch()
     need = gguf_size(qtype, N, K)
     if isinstance(gguf, np.ndarray):
         gguf = torch.from_numpy(np.ascontiguousarray(gguf).view(np.uint8).reshape(-1))
     if gguf.numel() * gguf.element_size() < need:
         raise QGemmError(-1, "weights buffer is smaller than N * K/group * sizeof(block)")
+    if out is not None:
+        if out.dtype != torch.uint8 or out.dim() != 1 or not out.is_contiguous() or \
+                out.numel() != packed_size(qtype, N, K) or out.device.type != "cuda":
+            raise QGemmError(-1, "out must be a contiguous uint8 device tensor of packed_size bytes")
+        device = out.device
     with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
-        buf = torch.empty(packed_size(qtype, N, K), dtype=torch.uint8, device=device)
+        buf = out if out is not None else torch.empty(packed_size(qtype, N, K), dtype=torch.uint8, device=device)
         if gguf.device.type == "cpu":
             gguf = gguf.to(device, non_blocking=False)
         elif not gguf.is_contiguous():
@@ -350,3 +363,65 @@ def q_gemm_swiglu(input, gate, up, out=None, out_dtype=None, stream=None, worksp
                                    _stream_ptr(stream)))
     return out
 
+
+
+class MlpWorkspace:
+    """Device workspace of the fused MLP (mlxr_qgemm_mlp): sync words (zeroed once here, left
+    zero by every launch), the gated intermediate h, split-K partials.  Grows on demand;
+    calls that share one must not overlap."""
+
+    def __init__(self, device):
+        self.device, self.buf = device, None
+
+    def get(self, nbytes, stream=None):
+        torch = _torch()
+        if self.buf is None or self.buf.numel() < nbytes:
+            with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+                self.buf = torch.empty(max(nbytes, MLP_H_OFFSET), dtype=torch.uint8, device=self.device)
+            _check(lib().mlxr_qgemm_mlp_workspace_init(self.buf.data_ptr(), self.buf.numel(), _stream_ptr(stream)))
+        return self.buf
+
+    def status(self, stream=None):
+        """Raises QGemmError (MLXR_E_TIMEOUT) if a launch on this workspace gave up its wait."""
+        if self.buf is not None:
+            _check(lib().mlxr_qgemm_mlp_status(self.buf.data_ptr(), _stream_ptr(stream)))
+
+
+def mlp_workspace_size(qtype_gu, qtype_down, hidden, inter, M):
+    n = ctypes.c_size_t(0)
+    _check(lib().mlxr_qgemm_mlp_workspace_size(int(qtype_gu), int(qtype_down), int(hidden), int(inter), int(M),
+                                               ctypes.byref(n)))
+    return n.value
+
+
+def q_gemm_mlp(input, gate, up, down, workspace, out=None, out_dtype=None, stream=None, mode=MLP_AUTO):
+    """y = down . (swish(input . gate^T) * (input . up^T)) (mlxr_qgemm_mlp_ex): the fused
+    gate/up/gating launch and the down projection, or with mode=MLP_ONE_LAUNCH (M = 1) one
+    launch for the whole MLP.  ``workspace`` is an MlpWorkspace."""
+    torch = _torch()
+    M, H = input.shape
+    if (gate.qtype, gate.N, gate.K) != (up.qtype, up.N, up.K) or gate.K != H:
+        raise QGemmError(-3, "gate and up must be packed weights of the same type and [inter, hidden]")
+    if (down.N, down.K) != (H, gate.N):
+        raise QGemmError(-3, "down must be a packed [hidden, inter] weight")
+    if not input.is_contiguous():
+        input = input.contiguous()
+    if out is None:
+        out = torch.empty((M, H), dtype=out_dtype or input.dtype, device=input.device)
+    _check_out(out, M, H, input.device)
+    need = mlp_workspace_size(gate.qtype, down.qtype, H, gate.N, M)
+    ws = workspace.get(need, stream)
+    _check(lib().mlxr_qgemm_mlp_ex(int(gate.qtype), int(down.qtype), H, gate.N, gate.data_ptr(), up.data_ptr(),
+                                   down.data_ptr(), input.data_ptr(), _dt_code(input.dtype), out.data_ptr(),
+                                   _dt_code(out.dtype), M, int(mode), ws.data_ptr(), ws.numel(), _stream_ptr(stream)))
+    return out
+
+
+def test_set_operand_limit(nbytes):
+    """Test hook: lower the 2 GiB single-launch operand limit (0 restores it)."""
+    _check(lib().mlxr_qgemm_test_set_operand_limit(int(nbytes)))
+
+
+def test_set_mlp_spin_limit(ticks):
+    """Test hook: the fused MLP's wait bound in 100 MHz ticks (0 restores 0.2 s)."""
+    _check(lib().mlxr_qgemm_test_set_mlp_spin_limit(int(ticks)))

@@ -8,6 +8,7 @@
 // tests/test_layers.py checks against the oracle.  Prints "OK <n>" on success.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -91,6 +92,38 @@ int main(int argc, char** argv) {
     if (M == 3) dump(out_dir, "linear_m3.bin", yc);
   }
 
+  // The layer's split-K workspace used on a second stream and then grown there: the old
+  // buffer is released only after that stream's work, and results stay exact.
+  {
+    graph::Linear ls(4096, 1024, false);
+    std::vector<uint8_t> wl((size_t)1024 * 4096 / 256 * 144);
+    mlxr_synth_gguf(MLXR_Q4_K, 1024, 4096, 78, wl.data());
+    ls.load_weight(wl.data(), QuantType::Q4_K);
+    hipStream_t sa, sb;
+    EXPECT(hipStreamCreate(&sa) == hipSuccess && hipStreamCreate(&sb) == hipSuccess);
+    array xa = act(40, 4096, 31), xb = act(300, 4096, 32);
+    hipDeviceSynchronize();
+    for (int rep = 0; rep < 2; ++rep) {
+      array ya = ls.forward(xa, kernels::Stream{sa});  // allocates the workspace on sa
+      EXPECT(hipStreamSynchronize(sa) == hipSuccess);
+      array yb = ls.forward(xa, kernels::Stream{sb});  // reuses it on sb
+      array yg = ls.forward(xb, kernels::Stream{sb});  // grows it: frees sa's buffer after sb's work
+      EXPECT(hipStreamSynchronize(sb) == hipSuccess);
+      // references: the caller-owned forward with its own workspace (same split plans)
+      array ra({40, 1024}, Dtype::bfloat16), rg({300, 1024}, Dtype::bfloat16);
+      const size_t wr = std::max(ls.workspace_size(40), ls.workspace_size(300));
+      array wref({(int)wr + 1}, Dtype::uint8);
+      ls.forward(xa, ra, wref.data<void>(), wr);
+      ls.forward(xb, rg, wref.data<void>(), wr);
+      hipDeviceSynchronize();
+      EXPECT(to_host(ya) == to_host(ra) && to_host(yb) == to_host(ra) && to_host(yg) == to_host(rg));
+      ls = graph::Linear(4096, 1024, false);  // fresh layer (empty workspace) for the second round
+      ls.load_weight(wl.data(), QuantType::Q4_K);
+    }
+    hipStreamDestroy(sa);
+    hipStreamDestroy(sb);
+  }
+
   if (gguf_path) {
     mlxr_gguf* g = nullptr;
     EXPECT(mlxr_gguf_open(gguf_path, &g) == 0);
@@ -121,7 +154,7 @@ int main(int argc, char** argv) {
   mlp.gate_proj().load_weight(wg.data(), QuantType::Q4_K);
   mlp.up_proj().load_weight(wu.data(), QuantType::Q4_K);
   mlp.down_proj().load_weight(wd.data(), QuantType::Q4_K);
-  for (int M : {2, 24, 100}) {
+  for (int M : {1, 2, 24, 100}) {
     array x = act(M, H, 50 + M);
     array y = mlp.forward(x);
     array h({M, I}, Dtype::bfloat16);

@@ -298,7 +298,7 @@ def test_mfma_few_tiles_long_k(cuda, qt, M, N, K):
     assert orc.rel_err(y1.cpu().numpy(), ref) <= TOL
 
 
-def test_mfma_chunked_launches(cuda, monkeypatch):
+def test_mfma_chunked_launches(cuda):
     """Operands past the 32-bit offset range run as several launches over M and N chunks;
     a lowered chunk limit makes small shapes take that path (three M chunks, three N
     chunks), which must stay within tolerance like the single launch."""
@@ -307,15 +307,18 @@ def test_mfma_chunked_launches(cuda, monkeypatch):
     w, pw = _packed(torch, qt, N, K, 141, cuda)
     x, xf = _act(torch, M, K, mx.BF16, 142, cuda)
     y1 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
-    monkeypatch.setenv("MLXR_MFMA_CHUNK_BYTES", str(1 << 17))  # 256-row and 256-column chunks
-    y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    mx.qgemm.test_set_operand_limit(1 << 17)  # 256-row and 256-column chunks
+    try:
+        y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    finally:
+        mx.qgemm.test_set_operand_limit(0)
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
     assert orc.rel_err(y2.cpu().numpy(), ref) <= TOL
     assert orc.rel_err(y1.cpu().numpy(), ref) <= TOL
 
 
 @pytest.mark.parametrize("M", [8, 40])
-def test_skinny_operand_limit_falls_back_to_chunked_tiles(cuda, monkeypatch, M):
+def test_skinny_operand_limit_falls_back_to_chunked_tiles(cuda, M):
     """The skinny kernels address every operand with 32-bit offsets: when a weight plane
     reaches the limit (lowered here so that a small shape does) the call runs on the tiled
     kernel's chunked launches instead, and stays within tolerance; grouped calls and the
@@ -326,14 +329,17 @@ def test_skinny_operand_limit_falls_back_to_chunked_tiles(cuda, monkeypatch, M):
     x, xf = _act(torch, M, K, mx.BF16, 152 + M, cuda)
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
     y1 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
-    monkeypatch.setenv("MLXR_MFMA_CHUNK_BYTES", str(1 << 17))  # below the 358 KB qs plane
-    y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
-    ys = mx.q_gemm_dequant_grouped(x, [pw, pw], out_dtype=torch.float32)
+    mx.qgemm.test_set_operand_limit(1 << 17)  # below the 358 KB qs plane
+    try:
+        y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+        ys = mx.q_gemm_dequant_grouped(x, [pw, pw], out_dtype=torch.float32)
+        wu = mx.synth_gguf(qt, N, K, 161 + M)
+        pu = mx.pack_weights(wu, N, K, qt, device=cuda)
+        h = mx.q_gemm_swiglu(x, pw, pu, out_dtype=torch.float32)
+    finally:
+        mx.qgemm.test_set_operand_limit(0)
     for y in (y1, y2, ys[0], ys[1]):
         assert orc.rel_err(y.cpu().numpy(), ref) <= TOL
-    wu = mx.synth_gguf(qt, N, K, 161 + M)
-    pu = mx.pack_weights(wu, N, K, qt, device=cuda)
-    h = mx.q_gemm_swiglu(x, pw, pu, out_dtype=torch.float32)
     g = ref.astype(np.float64)
     u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=True).astype(np.float64)
     assert orc.rel_err(h.cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= TOL
