@@ -50,6 +50,22 @@ std::atomic<size_t> g_operand_limit{(size_t)1 << 31};
 
 size_t operand_limit() { return g_operand_limit.load(std::memory_order_relaxed); }
 
+size_t device_lds_limit() {
+  constexpr int kDev = 64;
+  static std::atomic<uint32_t> cache[kDev];  // 0: not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev) return 64 * 1024;
+  uint32_t v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int a = 0;
+    if (hipDeviceGetAttribute(&a, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess || a <= 0)
+      a = 64 * 1024;
+    v = (uint32_t)std::min(a, 160 * 1024);
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 int set_error(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;

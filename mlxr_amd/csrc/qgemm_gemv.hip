@@ -333,8 +333,7 @@ __global__ __launch_bounds__(256) void qgemv_lds_kernel(LdsParams lp) {
 size_t lds_bytes(int MT, int K) { return (size_t)MT * (size_t)(((K >> 5) + 63) >> 6) * 64 * 72; }
 
 // gfx950 gives a workgroup up to 160 KiB of LDS (above 64 KiB once the kernel's limit
-// is raised).
-constexpr size_t kMaxLds = 160 * 1024;
+// is raised); device_lds_limit() is that figure as the device reports it.
 
 int num_cus() {
   static int cus = 0;
@@ -368,7 +367,8 @@ hipError_t allow_lds(KernelPtr k, size_t bytes, std::atomic<uint64_t>& done) {
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   const uint64_t bit = 1ull << (dev & 63);
   if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
-  const hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+  const hipError_t e =
+      hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)device_lds_limit());
   if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
   return e;
 }
@@ -402,7 +402,7 @@ bool lds_fits(int M, int K, const PackedLayout& L, int MT) {
   for (int i = 0; i < L.nplanes; ++i)
     if (L.size[i] >= lim) return false;
   if ((size_t)M * K * 2 >= lim) return false;
-  return lds_bytes(MT, K) <= kMaxLds;
+  return lds_bytes(MT, K) <= device_lds_limit();
 }
 
 int mt_for(int M) { return M == 1 ? 1 : M <= 2 ? 2 : 4; }

@@ -66,6 +66,9 @@ size_t mfma_grouped_workspace_bytes(const RunArgs* const* items, int n);
 // launch: 2 GiB.  Test hook: mlxr_qgemm_test_set_operand_limit lowers it (an atomic), so the
 // tests reach the chunked and fallback launches at small sizes.
 size_t operand_limit();
+// LDS a workgroup may use on the current device once a kernel's limit is raised: the
+// device's opt-in maximum, at most 160 KiB (gfx950), queried once per device.
+size_t device_lds_limit();
 
 // Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.  With a.ws,
 // shapes with fewer 32-row slabs than CUs also split K over workgroups.

@@ -453,7 +453,6 @@ int num_cus_dev() {
 
 size_t act_lds_bytes(int K) { return (size_t)(((K >> 5) + 63) >> 6) * 64 * 72; }
 
-constexpr size_t kMlpMaxLds = 160 * 1024;
 std::atomic<uint32_t> g_spin_limit{20000000u};  // 0.2 s of the 100 MHz counter
 
 MlpRole role_of(const PackedLayout& L, const void* packed) {
@@ -474,7 +473,8 @@ hipError_t launch_t(const MlpParams& p, unsigned grid, size_t lds, hipStream_t s
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(attr.load(std::memory_order_acquire) & bit)) {
-      const hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMlpMaxLds);
+      const hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)device_lds_limit());
       if (e != hipSuccess) return e;
       attr.fetch_or(bit, std::memory_order_release);
     }
@@ -514,7 +514,7 @@ bool mlp_fused_ok(const MlpArgs& a) {
   for (const PackedLayout* L : {&a.gate, &a.up, &a.down})
     for (int i = 0; i < L->nplanes; ++i)
       if (L->size[i] >= lim) return false;
-  return act_lds_bytes(a.H) <= kMlpMaxLds && (size_t)a.H * 2 < lim && (size_t)a.I * 2 < lim;
+  return act_lds_bytes(a.H) <= device_lds_limit() && (size_t)a.H * 2 < lim && (size_t)a.I * 2 < lim;
 }
 
 hipError_t launch_mlp_fused(const MlpArgs& a, hipStream_t s) {

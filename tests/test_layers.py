@@ -167,11 +167,12 @@ def test_q_gemm_swiglu_matches_oracle(cuda, qt, M):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N", [(130, 300), (257, 258), (300, 130)])
+@pytest.mark.parametrize("M,N", [(130, 300), (257, 258), (300, 130), (8, 250), (30, 77), (5, 16), (17, 33)])
 def test_q_gemm_swiglu_ragged_tiles(cuda, M, N):
-    """The fused tiled kernel where the tile edges cut rows and columns: N not a multiple of
-    the 128-column SwiGLU tile, N % 4 != 0 (scalar stores), M not a multiple of 32, split
-    and unsplit, bf16 and fp32 outputs."""
+    """The fused kernels where the tile edges cut rows and columns: N not a multiple of the
+    128-column SwiGLU tile (tiled kernel, M > 32) or of the 16-row slab (narrow skinny
+    kernel, M <= 32), N % 4 != 0 (scalar stores), M not a multiple of 32, split and unsplit,
+    bf16 and fp32 outputs."""
     import torch
     qt, K = mx.QuantType.Q4_K, 1024
     wg, wu = mx.synth_gguf(qt, N, K, 81), mx.synth_gguf(qt, N, K, 82)
