@@ -63,10 +63,12 @@ enum {
 /* Execution path selector for mlxr_qgemm_run_ex. */
 enum {
   MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M <= 4; MFMA kernels above: skinny (weights
-                         streamed once) for M <= 64, tiled GEMM beyond -- and from M = 33
-                         when mlxr_qgemm_run_ws is given the workspace it asks for */
+                         streamed once) for M <= 64, tiled GEMM beyond.  When
+                         mlxr_qgemm_run_ws is given the workspace it asks for, calls with
+                         32 < M <= 256 take whichever of the two is estimated faster for
+                         the shape (the skinny one for narrow weights) */
   MLXR_PATH_GEMV = 1, /* force the wavefront-reduction GEMV kernel (any M <= 64) */
-  MLXR_PATH_MFMA = 2  /* force the MFMA kernels (skinny for M <= 64, tiled above) */
+  MLXR_PATH_MFMA = 2  /* force the MFMA kernels (chosen as for MLXR_PATH_AUTO) */
 };
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -127,8 +129,9 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
  * problem would not use one.  MFMA GEMMs whose workgroups would be too few to fill the
  * device (tiled ones, M > 32, and skinny ones with few 32-row slabs) split K over several
  * workgroups and add the fp32 partials in a second kernel; the workspace holds those
- * partials (splits x M x N x 4 bytes).  For 32 < M <= 64 a workspace also moves the call
- * from the skinny kernel to the tiled one (64-row tiles).
+ * partials (splits x M x N x 4 bytes).  For 32 < M <= 256 the size is that of the kernel
+ * the call would choose with it; mlxr_qgemm_run_ws ignores a smaller workspace (the call
+ * then runs as mlxr_qgemm_run_ex: skinny kernel for M <= 64, tiled one above, unsplit).
  * No counterpart in the reference (its kernel has no K split, q_gemm_dequant.metal:374-464). */
 int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes);
 
@@ -251,9 +254,13 @@ int mlxr_qgemm_mlp_status(void* workspace_dev, void* stream);
  * one launch (default 2 GiB; 0 restores it), lowered by tests so small shapes reach the
  * chunked and fallback launches.  mlxr_qgemm_test_set_mlp_spin_limit: the fused MLP's wait
  * bound in ticks of the 100 MHz real-time counter (default 0.2 s; 0 restores it), lowered
- * by tests to exercise the timeout path.  Both are process-wide (atomics). */
+ * by tests to exercise the timeout path.  mlxr_qgemm_test_force_skinny(1): every call of the
+ * MFMA family (M > 4, or MLXR_PATH_MFMA) runs the skinny kernel, at any M, until called
+ * with 0; tests use it to reach the skinny kernel's 64-row M blocks at shapes the automatic
+ * choice gives to the tiled kernel.  All are process-wide (atomics). */
 int mlxr_qgemm_test_set_operand_limit(size_t bytes);
 int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks);
+int mlxr_qgemm_test_force_skinny(int on);
 
 /* Deterministic synthetic inputs with the shapes/distributions of the benchmark
  * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by

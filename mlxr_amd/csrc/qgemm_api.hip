@@ -26,6 +26,24 @@ constexpr int kGemvMaxM = 4;
 // and down 26.7 vs 29.7 us; at M = 64 the tiled one, gate 28.3 vs 42.7 us).
 constexpr int kSkinnyOnlyMaxM = 32;
 int skinny_only_max_m() { return kSkinnyOnlyMaxM; }
+// Up to this M a single call chooses between the skinny kernel (in 64-row blocks of M)
+// and the tiled one by their estimated times: on MI355X the skinny one wins for narrow
+// weights, e.g. Llama-3-8B k/v at M = 128: 12.3 against 18.6 us.
+constexpr int kSkinnyMaxM = 256;
+
+// For skinny_only_max_m() < M <= kSkinnyMaxM: whether the skinny kernel serves a call that
+// has the workspace the library asks for (ws) or none.  Without one the skinny kernel
+// takes M <= 64 and the tiled one (unsplit) larger M.
+bool skinny_mid(int M, const mlxr::PackedLayout& L, bool ws) {
+  if (!ws) return M <= 64;
+  return mlxr::skinny_mb_est_us(M, L.N, L.K) < mlxr::mfma_est_us(M, L.N, L.K, ~(size_t)0);
+}
+// The workspace size for those M: that of the kernel skinny_mid picks with one.
+void mid_workspace(int M, const mlxr::PackedLayout& L, size_t* bytes) {
+  *bytes = skinny_mid(M, L, true) ? mlxr::skinny_workspace_bytes(M, L.N, L.K, L.qtype)
+                                  : mlxr::mfma_workspace_bytes(M, L.N, L.K);
+}
+std::atomic<int> g_force_skinny{0};
 
 thread_local std::string g_err;
 
@@ -194,9 +212,12 @@ int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes) {
   if (rc) return rc;
   if (!bytes) return fail(MLXR_E_INVALID, "null output pointer");
   if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
-  *bytes = M > skinny_only_max_m() ? mlxr::mfma_workspace_bytes(M, N, K)
-          : M > kGemvMaxM      ? mlxr::skinny_workspace_bytes(M, N, K, qtype)
-                               : 0;
+  if (M > skinny_only_max_m() && M <= kSkinnyMaxM)
+    mid_workspace(M, L, bytes);
+  else
+    *bytes = M > skinny_only_max_m() ? mlxr::mfma_workspace_bytes(M, N, K)
+             : M > kGemvMaxM         ? mlxr::skinny_workspace_bytes(M, N, K, qtype)
+                                     : 0;
   return MLXR_OK;
 }
 
@@ -240,12 +261,22 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   // tiled one above -- and from M = 33 when a workspace lets it split K
   // (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
   const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= kGemvMaxM);
+  // the skinny kernels address operands with 32-bit offsets; the tiled launcher splits
+  // larger problems into chunks
   bool skinny = false;
-  if (!gemv && M <= 64) {
-    const size_t need = M > skinny_only_max_m() ? mlxr::mfma_workspace_bytes(M, a.L.N, a.L.K) : 0;
-    // the skinny kernels address operands with 32-bit offsets; the tiled launcher splits
-    // larger problems into chunks
-    skinny = (need == 0 || !a.ws || a.ws_bytes < need) && mlxr::skinny_fits(a);
+  if (!gemv && g_force_skinny.load(std::memory_order_relaxed)) {
+    skinny = mlxr::skinny_fits(a);
+  } else if (!gemv && M <= skinny_only_max_m()) {
+    skinny = mlxr::skinny_fits(a);
+  } else if (!gemv && M <= kSkinnyMaxM) {
+    // a workspace below the size mlxr_qgemm_workspace_size asks for is not used
+    size_t need = 0;
+    mid_workspace(M, a.L, &need);
+    if (!a.ws || a.ws_bytes < need) {
+      a.ws = nullptr;
+      a.ws_bytes = 0;
+    }
+    skinny = mlxr::skinny_fits(a) && skinny_mid(M, a.L, a.ws != nullptr);
   }
   hipError_t e;
   if (gemv) e = mlxr::launch_gemv(a, (hipStream_t)stream);
@@ -617,6 +648,11 @@ int mlxr_qgemm_mlp_status(void* workspace_dev, void* stream) {
 
 int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks) {
   mlxr::set_mlp_spin_limit(ticks ? ticks : 20000000u);
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_test_force_skinny(int on) {
+  g_force_skinny.store(on ? 1 : 0, std::memory_order_relaxed);
   return MLXR_OK;
 }
 

@@ -99,6 +99,10 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
   const int nkt = (K + TK - 1) / TK;
   const int ksplit = blockIdx.x / p.slabs;
   const int n0 = (blockIdx.x - ksplit * p.slabs) * 32;
+  // M-block blockIdx.y: activation rows [m0, m0 + 64), addressed from its own base
+  const int m0 = blockIdx.y * 64, Mt = M;
+  const int Ml = min(64, Mt - m0);
+  const uint16_t* const xb = (const uint16_t*)p.x + (size_t)m0 * (size_t)K;
   const int h = lane >> 5, n = n0 + (lane & 31);
   const bool rok = n < N;
   const uint32_t row_sub = rok ? (uint32_t)n * (uint32_t)nsub : 0u, row_sb = rok ? (uint32_t)n * (uint32_t)nsb : 0u;
@@ -107,15 +111,15 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
   rsrc_t R[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) R[i] = make_rsrc(p.P.p[i] ? p.P.p[i] : (const uint8_t*)p.x, p.psize[i]);
-  const rsrc_t RX = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+  const rsrc_t RX = make_rsrc(xb, (uint32_t)Ml * (uint32_t)K * 2u);
 
-  // activation rows of the second operand: mb*32 + lane%32; lane half h reads K
+  // activation rows of the second operand: m0 + mb*32 + lane%32; lane half h reads K
   // positions 32h + 8kk .. +7 of each step (kk at immediate offset 16kk)
   uint32_t xoff[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = mb * 32 + (lane & 31);
-    xoff[mb] = m < M ? ((uint32_t)m * (uint32_t)K + 32u * h) * 2u : OOB;
+    xoff[mb] = m < Ml ? ((uint32_t)m * (uint32_t)K + 32u * h) * 2u : OOB;
   }
   const int ktail = K % TK;  // the 32-weight block types can end on a half step
   u32x4_t xf[4][4][MB];  // ring: step s in slot s % 4
@@ -195,8 +199,8 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
   // wavefront w finishes M-blocks w, w + nw, ... (a workgroup may have fewer wavefronts
   // than M-blocks when K is short)
   for (int mb = wave; mb < MB; mb += nw) {
-    const int m = mb * 32 + (lane & 31);
-    if (m >= M) continue;
+    const int m = m0 + mb * 32 + (lane & 31);
+    if (m >= Mt) continue;
     float out[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -510,10 +514,10 @@ int device_cus_s() {
 struct SkinnyPlan {
   int ks, spg, w, spw;
 };
-SkinnyPlan skinny_plan(int N, int K, int ring, bool allow_split) {
+SkinnyPlan skinny_plan(int N, int K, int ring, bool allow_split, int mblocks = 1) {
   constexpr int wpc = 8;  // wavefronts per CU aimed for
   const int cus = device_cus_s();
-  const int slabs = (N + 31) / 32;
+  const int slabs = (N + 31) / 32 * mblocks;  // workgroups per K split
   const int nkt = (K + TK - 1) / TK;
   SkinnyPlan pl;
   pl.ks = allow_split && slabs < cus ? std::max(1, std::min(cus / slabs, nkt / ring)) : 1;
@@ -594,8 +598,10 @@ hipError_t launch_s(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   if (use_skinny16(sp.M)) return launch_s16<QT, XT>(sp, ws_bytes, s);
   constexpr int RING = ring_steps<QT>();
   sp.slabs = (sp.N + 31) / 32;
-  SkinnyPlan pl = skinny_plan(sp.N, sp.K, RING, sp.ws != nullptr);
-  if (pl.ks > 1 && (size_t)pl.ks * (size_t)sp.M * (size_t)sp.N * 4u > ws_bytes) pl = skinny_plan(sp.N, sp.K, RING, false);
+  const int mblocks = (sp.M + 63) / 64;
+  SkinnyPlan pl = skinny_plan(sp.N, sp.K, RING, sp.ws != nullptr, mblocks);
+  if (pl.ks > 1 && (size_t)pl.ks * (size_t)sp.M * (size_t)sp.N * 4u > ws_bytes)
+    pl = skinny_plan(sp.N, sp.K, RING, false, mblocks);
   sp.spg = pl.spg;
   sp.spw = pl.spw;
   sp.ws_ld = sp.N;
@@ -604,7 +610,7 @@ hipError_t launch_s(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   void* const y = sp.y;
   const void* const bias = sp.bias;
   if (pl.ks == 1) sp.ws = nullptr;
-  const dim3 grid((unsigned)(sp.slabs * pl.ks)), block((unsigned)(64 * pl.w));
+  const dim3 grid((unsigned)(sp.slabs * pl.ks), (unsigned)mblocks), block((unsigned)(64 * pl.w));
   if (sp.M <= 32) qgemm_skinny_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
   else qgemm_skinny_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);
   hipError_t e = hipGetLastError();
@@ -702,8 +708,15 @@ bool skinny_fits(const RunArgs& a) {
   return true;
 }
 
+double skinny_mb_est_us(int M, int N, int K) {
+  // each 32-row slab reads its 64-row blocks of X from L2 (~7.5 TB/s device-wide), plus
+  // ~8 us of launch, prologue and epilogue (measured on MI355X, Llama-3-8B shapes)
+  return 8.0 + (double)((N + 31) / 32) * M * K * 2.0 / 7.5e6;
+}
+
 size_t skinny_workspace_bytes(int M, int N, int K, int qtype) {
-  const SkinnyPlan pl = use_skinny16(M) ? skinny16_plan(N, K, true, UNROLL16, MAXW, 8) : skinny_plan(N, K, qtype == QT_Q8_0 ? 4 : 8, true);
+  const SkinnyPlan pl = use_skinny16(M) ? skinny16_plan(N, K, true, UNROLL16, MAXW, 8)
+                                         : skinny_plan(N, K, qtype == QT_Q8_0 ? 4 : 8, true, (M + 63) / 64);
   return pl.ks > 1 ? (size_t)pl.ks * (size_t)M * (size_t)N * 4u : 0;
 }
 

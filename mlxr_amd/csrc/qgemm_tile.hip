@@ -404,6 +404,17 @@ hipError_t launch_splitk_reduce_swiglu(const float* ws, size_t split_elems, int 
   return hipGetLastError();
 }
 
+double mfma_est_us(int M, int N, int K, size_t ws_bytes) {
+  const SplitPlan sp = plan_split(M, N, K, ws_bytes);
+  const int nkt = (K + TK - 1) / TK;
+  const long rounds = ((long)sp.tiles * sp.S + device_cus() - 1) / device_cus();
+  double t = (double)rounds * (sp.kps * (sp.bm == 256 ? 1.0 : sp.bm == 128 ? 0.64 : 0.5) + 0.8);
+  if (sp.S > 1) t += (3.0 + (double)sp.S * M * N * 8.0 / 5e6) / 1.86;
+  // launches of one ring per workgroup take about 4.5 us more than the model says
+  // (measured on MI355X, Llama-3-8B q/k shapes at M = 64-512)
+  return t * 1.86 + (sp.kps <= 8 && nkt > 8 ? 4.5 : 0.0);
+}
+
 size_t mfma_workspace_bytes(int M, int N, int K) {
   if ((size_t)M * (size_t)K * 2u >= ((size_t)1 << 31)) return 0;
   const SplitPlan sp = plan_split(M, N, K, ~(size_t)0);

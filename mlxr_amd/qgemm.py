@@ -86,6 +86,7 @@ _SIGS = {
     "mlxr_qgemm_mlp_status": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "mlxr_qgemm_test_set_operand_limit": (ctypes.c_int, [ctypes.c_size_t]),
     "mlxr_qgemm_test_set_mlp_spin_limit": (ctypes.c_int, [ctypes.c_uint]),
+    "mlxr_qgemm_test_force_skinny": (ctypes.c_int, [ctypes.c_int]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
 }
@@ -425,3 +426,9 @@ def test_set_operand_limit(nbytes):
 def test_set_mlp_spin_limit(ticks):
     """Test hook: the fused MLP's wait bound in 100 MHz ticks (0 restores 0.2 s)."""
     _check(lib().mlxr_qgemm_test_set_mlp_spin_limit(int(ticks)))
+
+
+def test_force_skinny(on):
+    """Test hook: send every MFMA-family call to the skinny kernel (any M, in 64-row blocks
+    of M above 32) while on."""
+    _check(lib().mlxr_qgemm_test_force_skinny(1 if on else 0))

@@ -429,3 +429,54 @@ def test_python_binding_checks_outputs_and_bias(cuda):
     strided = torch.zeros(2 * N, device=cuda)[::2]
     y = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=strided, out_dtype=torch.float32)
     assert torch.equal(y, mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32))
+
+
+# The 32x32x16 skinny kernel in 64-row blocks of M (second grid dimension), forced at
+# shapes the automatic choice may give the tiled kernel: ragged last M block, ragged N,
+# every type, K not a multiple of 64 (Q8_0, Q4_0), split K through the workspace.
+@pytest.mark.parametrize("qt,M,N,K", [(Q4K, 65, 100, 768), (Q6K, 130, 257, 1024), (Q80, 200, 64, 1056),
+                                      (Q40, 96, 33, 96), (Q41, 256, 128, 2048), (Q5K, 129, 96, 512),
+                                      (Q4K, 300, 1024, 4096)])
+def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
+    import torch
+    w, pw = _packed(torch, qt, N, K, 171 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 181 + N, cuda)
+    bias = torch.linspace(-1, 1, N, device=cuda).to(torch.bfloat16)
+    mx.qgemm.test_force_skinny(True)
+    try:
+        y = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=torch.float32, path=mx.PATH_MFMA)
+        y2 = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    finally:
+        mx.qgemm.test_force_skinny(False)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bias.float().cpu().numpy(), w_to_bf16=True)
+    err = orc.rel_err(y.cpu().numpy(), ref)
+    # same bf16 weights as the oracle: only the fp32 accumulation order differs (K up to
+    # 4096 in up to eight split partials)
+    assert err <= 3e-5, err
+
+
+def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda):
+    """Llama-3-8B k shape at M = 128 with the workspace the library asks for: the automatic
+    choice is the skinny kernel (bit-equal to the forced skinny call); without a workspace
+    (M > 64) the tiled kernel runs unsplit; both within tolerance of the oracle."""
+    import torch
+    M, N, K = 128, 1024, 4096
+    w, pw = _packed(torch, Q4K, N, K, 191, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 192, cuda)
+    y_auto = mx.q_gemm_dequant(x, pw, M, N, K, Q4K, out_dtype=torch.float32)
+    mx.qgemm.test_force_skinny(True)
+    try:
+        y_sk = mx.q_gemm_dequant(x, pw, M, N, K, Q4K, out_dtype=torch.float32)
+    finally:
+        mx.qgemm.test_force_skinny(False)
+    y_ex = torch.empty((M, N), dtype=torch.float32, device=cuda)
+    rc = mx.lib().mlxr_qgemm_run_ex(int(Q4K), N, K, 0, pw.data_ptr(), x.data_ptr(), mx.BF16, None, mx.F32,
+                                    y_ex.data_ptr(), mx.F32, M, mx.PATH_AUTO, None)
+    assert rc == 0, mx.lib().mlxr_qgemm_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(y_auto, y_sk)
+    ref = orc.gemm_f64(int(Q4K), M, N, K, w, xf, w_to_bf16=True)
+    for y in (y_auto, y_ex):
+        assert orc.rel_err(y.cpu().numpy(), ref) <= 3e-5
