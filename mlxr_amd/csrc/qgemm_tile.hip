@@ -113,20 +113,47 @@ struct ReduceGroups {
   int col0[MAX_TG], N[MAX_TG], y_dtype[MAX_TG], bias_dtype[MAX_TG];
   int ngroups;
 };
+// VEC = 4 (every group's N a multiple of 4): four consecutive columns of one group per thread.
+template <int VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_grouped_kernel(const float* __restrict__ ws, size_t split_elems,
                                                                     int S, int ws_ld, size_t total, ReduceGroups rg) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
   if (i >= total) return;
-  float v = ws[i];
-  for (int sp = 1; sp < S; ++sp) v += ws[(size_t)sp * split_elems + i];
+  float v[VEC];
+  if constexpr (VEC == 4) {
+    const float4 a = *(const float4*)(ws + i);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    for (int sp = 1; sp < S; ++sp) {
+      const float4 b = *(const float4*)(ws + (size_t)sp * split_elems + i);
+      v[0] += b.x; v[1] += b.y; v[2] += b.z; v[3] += b.w;
+    }
+  } else {
+    v[0] = ws[i];
+    for (int sp = 1; sp < S; ++sp) v[0] += ws[(size_t)sp * split_elems + i];
+  }
   const int m = (int)(i / (size_t)ws_ld), c = (int)(i - (size_t)m * ws_ld);
   int g = 0;
 #pragma unroll
   for (int k = 1; k < MAX_TG; ++k)
     if (k < rg.ngroups && c >= rg.col0[k]) g = k;
   const int n = c - rg.col0[g];
-  if (rg.bias[g]) v += load_scalar(rg.bias[g], rg.bias_dtype[g], n);
-  store_scalar(rg.y[g], rg.y_dtype[g], (size_t)m * rg.N[g] + n, v);
+  if (rg.bias[g]) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] += load_scalar(rg.bias[g], rg.bias_dtype[g], n + e);
+  }
+  const size_t o = (size_t)m * rg.N[g] + n;
+  if constexpr (VEC == 4) {
+    const int yd = rg.y_dtype[g];
+    if (yd == DT_F32) {
+      *(float4*)((float*)rg.y[g] + o) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      const uint32_t lo = yd == DT_BF16 ? pack_bf16x2(v[0], v[1]) : pack2<X_F16>(v[0], v[1]);
+      const uint32_t hi = yd == DT_BF16 ? pack_bf16x2(v[2], v[3]) : pack2<X_F16>(v[2], v[3]);
+      *(uint2*)((uint16_t*)rg.y[g] + o) = make_uint2(lo, hi);
+    }
+  } else {
+    store_scalar(rg.y[g], rg.y_dtype[g], o, v[0]);
+  }
 }
 
 // SwiGLU split-K: the partial planes hold gate (columns 0 .. N-1) and up (N .. 2N-1) side
@@ -338,8 +365,14 @@ hipError_t launch_mfma_grouped(const RunArgs* const* items, int n, void* ws, siz
   hipError_t e = launch_chunk(tp, sp.bm, sp.S > 1 ? sp.S : 1, a.L.qtype, a.x_dtype == DT_F16, s);
   if (e != hipSuccess || sp.S <= 1) return e;
   const size_t total = (size_t)M * (size_t)cols;
-  splitk_reduce_grouped_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
-      (const float*)ws, tp.ws_split, sp.S, cols, total, rg);
+  bool vec4 = true;
+  for (int i = 0; i < n; ++i) vec4 = vec4 && (items[i]->L.N & 3) == 0;
+  if (vec4)
+    splitk_reduce_grouped_kernel<4><<<dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, s>>>(
+        (const float*)ws, tp.ws_split, sp.S, cols, total, rg);
+  else
+    splitk_reduce_grouped_kernel<1><<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s>>>(
+        (const float*)ws, tp.ws_split, sp.S, cols, total, rg);
   return hipGetLastError();
 }
 

@@ -261,6 +261,29 @@ def test_grouped_tiled_launches(cuda, M, K):
         assert orc.rel_err(y.cpu().numpy(), ref) <= TOL, i
 
 
+@pytest.mark.parametrize("ydt", ["bf16", "f32"])
+def test_grouped_split_reduce_vectorized(cuda, ydt):
+    """Grouped tiled launch split over K whose weights all have N % 4 == 0 (the reduce then
+    handles four columns per thread): within tolerance of the oracle with a bias on a middle
+    weight, deterministic, for bf16 and f32 outputs."""
+    import torch
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32}[ydt]
+    M, K = 130, 4096
+    Ns = [512, 132, 1024]
+    gg = [mx.synth_gguf(Q4K, N, K, 500 + i) for i, N in enumerate(Ns)]
+    ws = [mx.pack_weights(g, N, K, Q4K, device=cuda) for g, N in zip(gg, Ns)]
+    x, xf = _act(torch, M, K, mx.BF16, 510, cuda)
+    bias = torch.linspace(-1, 1, 132, device=cuda).to(torch.bfloat16)
+    biases = [None, bias, None]
+    ys = mx.q_gemm_dequant_grouped(x, ws, biases=biases, out_dtype=tdt)
+    ys2 = mx.q_gemm_dequant_grouped(x, ws, biases=biases, out_dtype=tdt)
+    for i, (y, y2) in enumerate(zip(ys, ys2)):
+        assert torch.equal(y, y2), i
+        ref = orc.gemm_f64(int(Q4K), M, Ns[i], K, gg[i], xf, w_to_bf16=True,
+                           bias=None if biases[i] is None else biases[i].float().cpu().numpy())
+        assert orc.rel_err(y.float().cpu().numpy(), ref) <= TOL, i
+
+
 def test_grouped_tiled_many_items_f16(cuda):
     """Five same-type weights (more than one launch holds: four, then one), fp16 activations
     and outputs, a K that ends on a half step (Q8_0, K % 64 == 32), with and without the
