@@ -134,6 +134,8 @@ def blib():
         lb.mlxr_bench_stream_read.restype = ctypes.c_int
         lb.mlxr_bench_stream_read.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                               ctypes.c_int, ctypes.c_void_p]
+        lb.mlxr_bench_empty.restype = ctypes.c_int
+        lb.mlxr_bench_empty.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         lb.mlxr_bench_mfma_peak.restype = ctypes.c_int
         lb.mlxr_bench_mfma_peak.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         _BLIB = lb
@@ -248,6 +250,27 @@ def stream_read_ms(cx, args, launches):
     return ms
 
 
+def empty_launch_ms(cx, args, nlaunch, grid=2048):
+    """Graph-replayed time of nlaunch launches of an empty kernel (grid workgroups of 256
+    threads): milliseconds per replay.  The per-launch cost the step's structure pays before
+    any bytes move."""
+    torch = cx.torch
+    lib = blib()
+
+    def seq():
+        st = cx.mx.qgemm._stream_ptr(None)
+        for _ in range(nlaunch):
+            bcheck(lib.mlxr_bench_empty(grid, None, st))
+
+    g = cx.graph(seq)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = cx.event_ms(lambda r: g.replay(), args.steps)
+    del g
+    return ms
+
+
 def copy_ms(cx, args, ranges):
     """Graph-replayed time of a sequence of device-to-device copies (hipMemcpyAsync through
     torch's copy_), one per launch: ranges = [(arena, offset, bytes)], each copied into one
@@ -352,6 +375,8 @@ def run_headline(cx, args, out):
     ms_copy = copy_ms(cx, args, [(A, span[ln][0], span[ln][1]) for A in arenas for ln, _ in LAUNCHES])
     copy_us = {ln: 1e3 * copy_ms(cx, args, [(arenas[r % len(arenas)], span[ln][0], span[ln][1]) for r in range(R)]) / R
                for ln, _ in LAUNCHES}
+    # the structure's own cost: as many empty launches as the step has
+    ms_empty = empty_launch_ms(cx, args, len(copies) * len(LAUNCHES))
     # one layer per graph (a graph launch per 4 kernels), for comparison
     graphs = [cx.graph(lambda W=W: step(W)) for W in copies[:8]]
     for c in range(args.warmup):
@@ -432,6 +457,14 @@ def run_headline(cx, args, out):
                 "GBps": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9, 1),
                 "frac_hbm": round(len(copies) * step_bytes / (ms_ceiling * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "gemv_step_vs_ceiling": round(ms_ceiling / ms_model, 4)},
+            "launch_floor": {
+                "what": "the same number of graph nodes (128) launching an empty kernel of 2048 workgroups: the "
+                        "per-launch cost of this structure before any bytes move; max_frac_hbm = the step's bytes at "
+                        "8 TB/s plus this floor",
+                "ms_per_step": round(ms_empty, 5),
+                "us_per_launch": round(1e3 * ms_empty / nlaunch, 3),
+                "max_frac_hbm": round((len(copies) * step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3)
+                                      / (len(copies) * step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3 + ms_empty), 4)},
             "copy_ceiling": {
                 "what": "the runtime's device-to-device copy (hipMemcpyAsync via torch copy_) of each launch's "
                         "packed weight bytes (one contiguous range per launch) in the same 128-launch graph; "
