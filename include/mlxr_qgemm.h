@@ -132,6 +132,7 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
  * partials (splits x M x N x 4 bytes).  For 32 < M <= 256 the size is that of the kernel
  * the call would choose with it; mlxr_qgemm_run_ws ignores a smaller workspace (the call
  * then runs as mlxr_qgemm_run_ex: skinny kernel for M <= 64, tiled one above, unsplit).
+ * When the size is 0 the call makes the same choice with or without a workspace.
  * No counterpart in the reference (its kernel has no K split, q_gemm_dequant.metal:374-464). */
 int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes);
 

@@ -36,7 +36,7 @@ constexpr int kSkinnyMaxM = 256;
 // takes M <= 64 and the tiled one (unsplit) larger M.
 bool skinny_mid(int M, const mlxr::PackedLayout& L, bool ws) {
   if (!ws) return M <= 64;
-  return mlxr::skinny_mb_est_us(M, L.N, L.K) < mlxr::mfma_est_us(M, L.N, L.K, ~(size_t)0);
+  return mlxr::skinny_mb_est_us(M, L.N, L.K) < mlxr::mfma_est_us(M, L.N, L.K, L.qtype, ~(size_t)0);
 }
 // The workspace size for those M: that of the kernel skinny_mid picks with one.
 void mid_workspace(int M, const mlxr::PackedLayout& L, size_t* bytes) {
@@ -269,14 +269,16 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   } else if (!gemv && M <= skinny_only_max_m()) {
     skinny = mlxr::skinny_fits(a);
   } else if (!gemv && M <= kSkinnyMaxM) {
-    // a workspace below the size mlxr_qgemm_workspace_size asks for is not used
+    // a workspace below the size mlxr_qgemm_workspace_size asks for is not used; a call
+    // whose size is 0 has what it asks for, with or without one
     size_t need = 0;
     mid_workspace(M, a.L, &need);
-    if (!a.ws || a.ws_bytes < need) {
+    const bool ws_ok = need == 0 || (a.ws && a.ws_bytes >= need);
+    if (!ws_ok) {
       a.ws = nullptr;
       a.ws_bytes = 0;
     }
-    skinny = mlxr::skinny_fits(a) && skinny_mid(M, a.L, a.ws != nullptr);
+    skinny = mlxr::skinny_fits(a) && skinny_mid(M, a.L, ws_ok);
   }
   hipError_t e;
   if (gemv) e = mlxr::launch_gemv(a, (hipStream_t)stream);

@@ -80,7 +80,7 @@ size_t skinny_workspace_bytes(int M, int N, int K, int qtype);
 // Estimated time of launch_skinny for M > 32 (64-row blocks of M over a second grid
 // dimension) and of launch_mfma with a workspace of ws_bytes, in microseconds.
 double skinny_mb_est_us(int M, int N, int K);
-double mfma_est_us(int M, int N, int K, size_t ws_bytes);
+double mfma_est_us(int M, int N, int K, int qtype, size_t ws_bytes);
 // SwiGLU, h = swish(x.gate^T + bias_g) * (x.up^T + bias_u) into gate.y, with gate and up
 // of one type and shape; gate.ws / ws (may be null) holds split-K partials.
 // Narrow skinny kernel (M <= 32, skinny_swiglu_ok) and tiled kernel (any M; operands

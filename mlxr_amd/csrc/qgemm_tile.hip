@@ -437,11 +437,14 @@ hipError_t launch_splitk_reduce_swiglu(const float* ws, size_t split_elems, int 
   return hipGetLastError();
 }
 
-double mfma_est_us(int M, int N, int K, size_t ws_bytes) {
+double mfma_est_us(int M, int N, int K, int qtype, size_t ws_bytes) {
   const SplitPlan sp = plan_split(M, N, K, ws_bytes);
   const int nkt = (K + TK - 1) / TK;
   const long rounds = ((long)sp.tiles * sp.S + device_cus() - 1) / device_cus();
-  double t = (double)rounds * (sp.kps * (sp.bm == 256 ? 1.0 : sp.bm == 128 ? 0.64 : 0.5) + 0.8);
+  // Q6_K steps dequantize more per weight: measured on MI355X (Llama-3-70B v, 1024x8192,
+  // M = 256) 40.6 us against 24.8 us for the Q4_K weight of the same shape
+  const double qf = qtype == QT_Q6_K ? 1.6 : 1.0;
+  double t = (double)rounds * (sp.kps * (sp.bm == 256 ? 1.0 : sp.bm == 128 ? 0.64 : 0.5) * qf + 0.8);
   if (sp.S > 1) t += (3.0 + (double)sp.S * M * N * 8.0 / 5e6) / 1.86;
   // launches of one ring per workgroup take about 4.5 us more than the model says
   // (measured on MI355X, Llama-3-8B q/k shapes at M = 64-512)

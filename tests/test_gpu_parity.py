@@ -480,26 +480,33 @@ def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
     assert err <= 3e-5, err
 
 
-def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda):
-    """Llama-3-8B k shape at M = 128 with the workspace the library asks for: the automatic
-    choice is the skinny kernel (bit-equal to the forced skinny call); without a workspace
-    (M > 64) the tiled kernel runs unsplit; both within tolerance of the oracle."""
+@pytest.mark.parametrize("qt,N,K", [(Q4K, 1024, 4096), (Q6K, 4096, 4096)])
+def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda, qt, N, K):
+    """Shapes at M = 128 whose estimated times favour the skinny kernel: Llama-3-8B k (the
+    skinny kernel splits K, so it asks for a workspace) and a Q6_K 4096x4096 weight (256
+    blocks fill the device: workspace size 0).  With the workspace the library asks for the
+    call is bit-equal to the forced skinny call; mlxr_qgemm_run_ex without a workspace makes
+    the same choice when the size is 0 and otherwise runs the tiled kernel unsplit; all
+    within tolerance of the oracle."""
     import torch
-    M, N, K = 128, 1024, 4096
-    w, pw = _packed(torch, Q4K, N, K, 191, cuda)
+    M = 128
+    w, pw = _packed(torch, qt, N, K, 191, cuda)
     x, xf = _act(torch, M, K, mx.BF16, 192, cuda)
-    y_auto = mx.q_gemm_dequant(x, pw, M, N, K, Q4K, out_dtype=torch.float32)
+    need = mx.workspace_size(qt, N, K, M)
+    y_auto = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32)
     mx.qgemm.test_force_skinny(True)
     try:
-        y_sk = mx.q_gemm_dequant(x, pw, M, N, K, Q4K, out_dtype=torch.float32)
+        y_sk = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32)
     finally:
         mx.qgemm.test_force_skinny(False)
     y_ex = torch.empty((M, N), dtype=torch.float32, device=cuda)
-    rc = mx.lib().mlxr_qgemm_run_ex(int(Q4K), N, K, 0, pw.data_ptr(), x.data_ptr(), mx.BF16, None, mx.F32,
+    rc = mx.lib().mlxr_qgemm_run_ex(int(qt), N, K, 0, pw.data_ptr(), x.data_ptr(), mx.BF16, None, mx.F32,
                                     y_ex.data_ptr(), mx.F32, M, mx.PATH_AUTO, None)
     assert rc == 0, mx.lib().mlxr_qgemm_last_error()
     torch.cuda.synchronize()
     assert torch.equal(y_auto, y_sk)
-    ref = orc.gemm_f64(int(Q4K), M, N, K, w, xf, w_to_bf16=True)
+    if need == 0:
+        assert torch.equal(y_ex, y_sk)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
     for y in (y_auto, y_ex):
         assert orc.rel_err(y.cpu().numpy(), ref) <= 3e-5
