@@ -20,10 +20,10 @@ namespace {
 
 // Largest M the automatic path sends to the GEMV kernel.
 constexpr int kGemvMaxM = 4;
-// Above this M (and up to 64) the tiled GEMM with 64-row tiles and split-K beats the
-// skinny kernel when the caller provides a workspace (measured on MI355X, Llama-3-8B FFN
-// shapes: at M = 32 the skinny kernel's 16x16x32 variant is ahead, gate 26.9 vs 29.0 us
-// and down 26.7 vs 29.7 us; at M = 64 the tiled one, gate 28.3 vs 42.7 us).
+// Up to this M the skinny kernel serves every MFMA call (measured on MI355X, Llama-3-8B
+// FFN shapes: at M = 32 its 16x16x32 variant is ahead of the tiled GEMM with 64-row tiles
+// and split-K, gate 26.9 vs 29.0 us and down 26.7 vs 29.7 us; at M = 64 the tiled one,
+// gate 28.3 vs 42.7 us).
 constexpr int kSkinnyOnlyMaxM = 32;
 int skinny_only_max_m() { return kSkinnyOnlyMaxM; }
 // Up to this M a single call chooses between the skinny kernel (in 64-row blocks of M)
@@ -257,8 +257,8 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   a.M = M;
   a.ws = workspace_dev;
   a.ws_bytes = workspace_dev ? workspace_bytes : 0;
-  // GEMV (no MFMA) for decode; MFMA kernels otherwise: the skinny one up to M = 64, the
-  // tiled one above -- and from M = 33 when a workspace lets it split K
+  // GEMV (no MFMA) for decode; MFMA kernels otherwise: the skinny one up to M = 32, then up
+  // to M = 256 the skinny or the tiled one (skinny_mid), the tiled one above
   // (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
   const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= kGemvMaxM);
   // the skinny kernels address operands with 32-bit offsets; the tiled launcher splits
