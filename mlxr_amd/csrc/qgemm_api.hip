@@ -68,6 +68,19 @@ std::atomic<size_t> g_operand_limit{(size_t)1 << 31};
 
 size_t operand_limit() { return g_operand_limit.load(std::memory_order_relaxed); }
 
+int device_cu_count() {
+  constexpr int kDev = 64;
+  static std::atomic<int> cache[kDev];  // 0: not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 size_t device_lds_limit() {
   constexpr int kDev = 64;
   static std::atomic<uint32_t> cache[kDev];  // 0: not queried yet

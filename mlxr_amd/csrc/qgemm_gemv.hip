@@ -335,19 +335,6 @@ size_t lds_bytes(int MT, int K) { return (size_t)MT * (size_t)(((K >> 5) + 63) >
 // gfx950 gives a workgroup up to 160 KiB of LDS (above 64 KiB once the kernel's limit
 // is raised); device_lds_limit() is that figure as the device reports it.
 
-int num_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-    else
-      cus = 256;
-  }
-  return cus;
-}
-
 // Wavefronts per CU the row split aims for.  Every workgroup stages all of X in LDS, so
 // for long rows (K >= 8192: down-projection shapes) fewer, longer-lived wavefronts win:
 // the X staging traffic halves (measured on MI355X: Llama-3-8B down 10.6 -> 9.9 us at
@@ -421,7 +408,7 @@ unsigned lds_setup(const RunArgs* const* items, int n, LdsParams& lp, size_t* by
   long total_rows = 0;
   for (int i = 0; i < n; ++i) total_rows += items[i]->L.N;
   // rows per wavefront: as few as keep ~waves_per_cu wavefronts per CU busy
-  const long target = (long)num_cus() * waves_per_cu_target(a0.L.K);
+  const long target = (long)device_cu_count() * waves_per_cu_target(a0.L.K);
   int rpw = (int)min((total_rows + target - 1) / target, (long)(64 / MT));  // row results: one per lane
   if (rpw < 1) rpw = 1;
   int ws = 0;
@@ -525,7 +512,7 @@ hipError_t launch_lds_swiglu(const RunArgs& gate, const RunArgs& up, hipStream_t
   lds_setup(items, 2, lp, &bytes);
   // every wavefront works on gate rows (and the same up rows): group 1 owns no wavefronts;
   // as many wavefronts as a grouped launch of the two weights would have
-  const long target = (long)num_cus() * waves_per_cu_target(gate.L.K);
+  const long target = (long)device_cu_count() * waves_per_cu_target(gate.L.K);
   lp.g[0].rows_per_wave = lp.g[1].rows_per_wave =
       (int)std::min<long>(64 / mt_for(gate.M), std::max<long>(1, (gate.L.N + target - 1) / target));
   lp.g[1].wave_start = 0x7fffffff;

@@ -66,6 +66,8 @@ size_t mfma_grouped_workspace_bytes(const RunArgs* const* items, int n);
 // launch: 2 GiB.  Test hook: mlxr_qgemm_test_set_operand_limit lowers it (an atomic), so the
 // tests reach the chunked and fallback launches at small sizes.
 size_t operand_limit();
+// Compute units of the current device, queried once per device.
+int device_cu_count();
 // LDS a workgroup may use on the current device once a kernel's limit is raised: the
 // device's opt-in maximum, at most 160 KiB (gfx950), queried once per device.
 size_t device_lds_limit();

@@ -437,20 +437,6 @@ __global__ void mlp_sync_zero_kernel(unsigned* sync) {
   for (int i = threadIdx.x; i < kMlpSyncWords; i += blockDim.x) sync[i] = 0u;
 }
 
-int num_cus_dev() {
-  static std::atomic<int> cus{0};
-  int c = cus.load(std::memory_order_relaxed);
-  if (c == 0) {
-    int dev = 0, v = 0;
-    c = (hipGetDevice(&dev) == hipSuccess &&
-         hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            ? v
-            : 256;
-    cus.store(c, std::memory_order_relaxed);
-  }
-  return c;
-}
-
 size_t act_lds_bytes(int K) { return (size_t)(((K >> 5) + 63) >> 6) * 64 * 72; }
 
 std::atomic<uint32_t> g_spin_limit{20000000u};  // 0.2 s of the 100 MHz counter
@@ -531,7 +517,7 @@ hipError_t launch_mlp_fused(const MlpArgs& a, hipStream_t s) {
   p.gate = role_of(a.gate, a.gate_packed);
   p.up = role_of(a.up, a.up_packed);
   p.down = role_of(a.down, a.down_packed);
-  const long cus = num_cus_dev();
+  const long cus = device_cu_count();
   // gate/up: about 16 wavefronts per CU, one row of gate and up each per iteration, the
   // iteration count chosen so the last iteration is (nearly) full
   const long target_a = cus * 16;

@@ -496,18 +496,6 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
   }
 }
 
-int device_cus_s() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, v = 0;
-    cus = (hipGetDevice(&dev) == hipSuccess &&
-           hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-              ? v
-              : 256;
-  }
-  return cus;
-}
-
 // Launch geometry: workgroups own 32-row slabs and, when the slabs are fewer than the CUs
 // and a workspace is allowed, a K range (ks splits, each a whole number of rings); inside
 // a workgroup the wavefronts split the range again, enough of them for about eight per CU.
@@ -516,7 +504,7 @@ struct SkinnyPlan {
 };
 SkinnyPlan skinny_plan(int N, int K, int ring, bool allow_split, int mblocks = 1) {
   constexpr int wpc = 8;  // wavefronts per CU aimed for
-  const int cus = device_cus_s();
+  const int cus = device_cu_count();
   const int slabs = (N + 31) / 32 * mblocks;  // workgroups per K split
   const int nkt = (K + TK - 1) / TK;
   SkinnyPlan pl;
@@ -535,7 +523,7 @@ SkinnyPlan skinny_plan(int N, int K, int ring, bool allow_split, int mblocks = 1
 // workgroups sized for about `wpc` wavefronts per CU.
 SkinnyPlan skinny16_plan(int N, int K, bool allow_split, int unroll, int wcap, int wpc) {
   const int maxw = std::max(1, std::min(wcap, MAXW));
-  const int cus = device_cus_s();
+  const int cus = device_cu_count();
   const int slabs = (N + 31) / 32;
   const int nkt = (K + TK16 - 1) / TK16;
   const long want = (long)wpc * cus;

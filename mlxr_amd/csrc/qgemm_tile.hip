@@ -22,13 +22,6 @@ namespace {
 
 using namespace tile;
 
-int device_cus() {
-  int dev = 0, v = 0;
-  if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-      v > 0)
-    return v;
-  return 256;
-}
 
 // Tile rows and K split of a launch, from a small cost model in units of one 256-row
 // tile step: a 128-row tile step costs 0.64 of it (the weight dequant is shared by half
@@ -41,7 +34,7 @@ struct SplitPlan {
   int bm, tiles, S, kps;
 };
 SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
-  const int nkt = (K + TK - 1) / TK, cus = device_cus();
+  const int nkt = (K + TK - 1) / TK, cus = device_cu_count();
   const long tn = (N + TN - 1) / TN;
   SplitPlan best{256, 0, 1, 0};
   double best_t = 1e30;
@@ -440,7 +433,7 @@ hipError_t launch_splitk_reduce_swiglu(const float* ws, size_t split_elems, int 
 double mfma_est_us(int M, int N, int K, int qtype, size_t ws_bytes) {
   const SplitPlan sp = plan_split(M, N, K, ws_bytes);
   const int nkt = (K + TK - 1) / TK;
-  const long rounds = ((long)sp.tiles * sp.S + device_cus() - 1) / device_cus();
+  const long rounds = ((long)sp.tiles * sp.S + device_cu_count() - 1) / device_cu_count();
   // Q6_K steps dequantize more per weight: measured on MI355X (Llama-3-70B v, 1024x8192,
   // M = 256) 40.6 us against 24.8 us for the Q4_K weight of the same shape
   const double qf = qtype == QT_Q6_K ? 1.6 : 1.0;
