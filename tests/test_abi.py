@@ -164,3 +164,21 @@ def test_workspace_queries():
                            qgemm.Item(Q4K, 4096, 2048, 0, None, None, 0, None, 2))
     n = ctypes.c_size_t(0)
     assert L.mlxr_qgemm_grouped_workspace_size(2, arr, 512, ctypes.byref(n)) == -3  # K differs
+
+
+def test_workspace_sizes_hold_whole_partial_planes():
+    """Across types, shapes and M (GEMV sizes, the skinny kernel's, the mid-M range where
+    the skinny and tiled kernels compete, prefill): the size is 0 or a whole number of
+    M x N fp32 partial planes, with at least two planes (a split); the same query twice
+    gives the same answer."""
+    qts = [int(q) for q in (mx.QuantType.Q4_K, mx.QuantType.Q6_K, mx.QuantType.Q8_0, mx.QuantType.Q4_0,
+                            mx.QuantType.Q4_1, mx.QuantType.Q5_K)]
+    for qt in qts:
+        for N, K in [(1024, 4096), (4096, 4096), (14336, 4096), (4096, 14336), (100, 768), (1000, 2048)]:
+            for M in [1, 4, 5, 8, 16, 32, 33, 64, 65, 100, 128, 200, 256, 257, 512, 2048]:
+                w = mx.workspace_size(qt, N, K, M)
+                assert w == mx.workspace_size(qt, N, K, M)
+                if M <= 4:
+                    assert w == 0, (qt, N, K, M, w)
+                assert w % (4 * M * N) == 0, (qt, N, K, M, w)
+                assert w == 0 or w // (4 * M * N) >= 2, (qt, N, K, M, w)
