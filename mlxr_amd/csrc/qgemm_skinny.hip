@@ -167,10 +167,10 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny_kernel(SkinnyParams p)
     load_x(kt + 2, std::integral_constant<int, (u + 2) & 3>());
     if constexpr (is_kquant(QT) && (u & 3) == 0) decode_hdr<QT>(hdr[u >> 2], h, sc);
     uint4 w[4];
-    w[0] = dequant_word<QT, XT, 0>(raw[u], sc, u & 3, p.nib);
-    w[1] = dequant_word<QT, XT, 1>(raw[u], sc, u & 3, p.nib);
-    w[2] = dequant_word<QT, XT, 2>(raw[u], sc, u & 3, p.nib);
-    w[3] = dequant_word<QT, XT, 3>(raw[u], sc, u & 3, p.nib);
+    w[0] = dequant_word<QT, XT, 0, true>(raw[u], sc, u & 3, p.nib);
+    w[1] = dequant_word<QT, XT, 1, true>(raw[u], sc, u & 3, p.nib);
+    w[2] = dequant_word<QT, XT, 2, true>(raw[u], sc, u & 3, p.nib);
+    w[3] = dequant_word<QT, XT, 3, true>(raw[u], sc, u & 3, p.nib);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
@@ -399,10 +399,10 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
       uint4 w[4];
-      w[0] = dequant_word<QT, XT, 0>(raw[ru][t], sc[t], u & 1, p.nib);
-      w[1] = dequant_word<QT, XT, 1>(raw[ru][t], sc[t], u & 1, p.nib);
-      w[2] = dequant_word<QT, XT, 2>(raw[ru][t], sc[t], u & 1, p.nib);
-      w[3] = dequant_word<QT, XT, 3>(raw[ru][t], sc[t], u & 1, p.nib);
+      w[0] = dequant_word<QT, XT, 0, true>(raw[ru][t], sc[t], u & 1, p.nib);
+      w[1] = dequant_word<QT, XT, 1, true>(raw[ru][t], sc[t], u & 1, p.nib);
+      w[2] = dequant_word<QT, XT, 2, true>(raw[ru][t], sc[t], u & 1, p.nib);
+      w[3] = dequant_word<QT, XT, 3, true>(raw[ru][t], sc[t], u & 1, p.nib);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll

@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   sfor<4>([&](auto KK) {
     constexpr int kk = decltype(KK)::value;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) bf[j][kk] = dequant_word<QT, XT, kk>(raw[0][j], sc[j], 0, p.nib);
+    for (int j = 0; j < 2; ++j) bf[j][kk] = dequant_word<QT, XT, kk, true>(raw[0][j], sc[j], 0, p.nib);
   });
   // stage 0 complete (every wavefront's DMA of it) before its first fragments are read
   vm_wait<2 * MI + rops(PD - 2) + rops(PD - 1)>();
@@ -363,8 +363,8 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
         constexpr int k = decltype(TK_)::value;
         if constexpr ((k * SPS) / 10 == ts) {
           constexpr int jw = k / 5, kq = k % 5;
-          if constexpr (kq == 0) word_prelude<QT, kk>(raw[un][jw], sc[jw], un & 3, p.nib, wt[jw]);
-          else nw[jw][kq - 1] = word_quarter<QT, XT, kk, kq - 1>(wt[jw], p.nib);
+          if constexpr (kq == 0) word_prelude<QT, kk, true>(raw[un][jw], sc[jw], un & 3, p.nib, wt[jw]);
+          else nw[jw][kq - 1] = word_quarter<QT, XT, kk, kq - 1, true>(wt[jw], p.nib);
         }
       });
       if constexpr (ts == SPS - 1) {

@@ -12,7 +12,10 @@
 //   Q4_0  (q - 8) * d                   (exact)
 //   Q4_1  fma(q, d, m)                  (q*d exact; one rounding)
 // (the products keep the sign of zero of the GGUF formulas, which an fma with an
-// offset term would not: fma(a, 32, -32a) is +0 for negative a)
+// offset term would not: fma(a, 32, -32a) is +0 for negative a).  The GEMM kernels take
+// the MM variant: for Q6_K, Q8_0 and Q4_0 it forms the same values with one fma
+// (fma(a, q, -c*a) rounds a*q - c*a, which is exactly a*(q - c), once), one operation per
+// weight fewer; only an exact zero may differ in sign, which no product sum can see.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -157,7 +160,7 @@ struct WordTmp {
   float a, c;
 };
 
-template <int QT, int kk>
+template <int QT, int kk, bool MM = false>
 __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>& s, int q, uint32_t nib,
                                              WordTmp<QT>& t) {
   if constexpr (QT == QT_Q4_K) {
@@ -185,7 +188,7 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
     t.u0 = w & nib;
     t.u1 = (w >> 4) & nib;
     t.a = f16_bits_to_f32(r.d & 0xffffu);
-    t.c = QT == QT_Q4_0 ? 8.f : f16_bits_to_f32(r.d >> 16);
+    t.c = QT == QT_Q4_0 ? (MM ? -8.f * t.a : 8.f) : f16_bits_to_f32(r.d >> 16);
   } else if constexpr (QT == QT_Q6_K) {
     uint32_t lw = r.ql[kk], hv = r.qh[kk >> 1];
     pin(lw);
@@ -193,7 +196,7 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
     t.u0 = lw;
     t.u1 = hv;
     t.a = (kk < 2) ? s.a[q] : s.b[q];
-    t.c = 32.f;
+    t.c = MM ? -32.f * t.a : 32.f;
   } else {
     uint32_t w0 = kk < 2 ? r.a[2 * kk] : r.b[2 * kk - 4];
     uint32_t w1 = kk < 2 ? r.a[2 * kk + 1] : r.b[2 * kk - 3];
@@ -202,11 +205,11 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
     t.u0 = w0 ^ 0x80808080u;
     t.u1 = w1 ^ 0x80808080u;
     t.a = f16_bits_to_f32(r.d & 0xffffu);
-    t.c = 128.f;
+    t.c = MM ? -128.f * t.a : 128.f;
   }
 }
 
-template <int QT, int XT, int kk, int qq>
+template <int QT, int XT, int kk, int qq, bool MM = false>
 __device__ __forceinline__ uint32_t word_quarter(const WordTmp<QT>& t, uint32_t nib) {
   if constexpr (QT == QT_Q4_K || QT == QT_Q5_K || QT == QT_Q4_1) {
     // u0 bytes: weights 0, 4, 1, 5; u1 bytes: 2, 6, 3, 7
@@ -217,27 +220,35 @@ __device__ __forceinline__ uint32_t word_quarter(const WordTmp<QT>& t, uint32_t 
   } else if constexpr (QT == QT_Q4_0) {
     const uint32_t v = (qq & 1) ? t.u1 : t.u0;
     const int sh = (qq & 2) ? 8 : 0;
+    if constexpr (MM)
+      return pack2<XT>(__builtin_fmaf(t.a, (float)((v >> sh) & 0xffu), t.c),
+                       __builtin_fmaf(t.a, (float)((v >> (16 + sh)) & 0xffu), t.c));
     return pack2<XT>(((float)((v >> sh) & 0xffu) - t.c) * t.a, ((float)((v >> (16 + sh)) & 0xffu) - t.c) * t.a);
   } else if constexpr (QT == QT_Q6_K) {
     constexpr int rs = 8 * (kk & 1) + 2 * qq - 4;
     const uint32_t hs = rs >= 0 ? (t.u1 >> rs) : (t.u1 << (-rs));
     const uint32_t v = ((t.u0 >> (4 * qq)) & (nib & 0x000F000Fu)) | (hs & 0x00300030u);
+    if constexpr (MM)
+      return pack2<XT>(__builtin_fmaf(t.a, (float)(v & 0xffu), t.c), __builtin_fmaf(t.a, (float)((v >> 16) & 0xffu), t.c));
     return pack2<XT>(t.a * ((float)(v & 0xffu) - t.c), t.a * ((float)((v >> 16) & 0xffu) - t.c));
   } else {
     // bytes hold q + 128 (sign bits flipped in the prelude)
     const uint32_t v = (qq < 2) ? t.u0 : t.u1;
     const int sh = (qq & 1) ? 16 : 0;
+    if constexpr (MM)
+      return pack2<XT>(__builtin_fmaf(t.a, (float)((v >> sh) & 0xffu), t.c),
+                       __builtin_fmaf(t.a, (float)((v >> (sh + 8)) & 0xffu), t.c));
     return pack2<XT>(((float)((v >> sh) & 0xffu) - t.c) * t.a, ((float)((v >> (sh + 8)) & 0xffu) - t.c) * t.a);
   }
 }
 
-// The whole word (dequant entry point, GEMM prologue).
-template <int QT, int XT, int kk>
+// The whole word (dequant entry point; MM: GEMM kernels).
+template <int QT, int XT, int kk, bool MM = false>
 __device__ __forceinline__ uint4 dequant_word(const Raw<QT>& r, const Scales<QT>& s, int q, uint32_t nib) {
   WordTmp<QT> t;
-  word_prelude<QT, kk>(r, s, q, nib, t);
-  return make_uint4(word_quarter<QT, XT, kk, 0>(t, nib), word_quarter<QT, XT, kk, 1>(t, nib),
-                    word_quarter<QT, XT, kk, 2>(t, nib), word_quarter<QT, XT, kk, 3>(t, nib));
+  word_prelude<QT, kk, MM>(r, s, q, nib, t);
+  return make_uint4(word_quarter<QT, XT, kk, 0, MM>(t, nib), word_quarter<QT, XT, kk, 1, MM>(t, nib),
+                    word_quarter<QT, XT, kk, 2, MM>(t, nib), word_quarter<QT, XT, kk, 3, MM>(t, nib));
 }
 
 // Plain (compiler-visible) loads of sub-block sb of row n and of its super-block header,
