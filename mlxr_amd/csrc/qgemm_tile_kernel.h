@@ -134,13 +134,15 @@ __global__ __launch_bounds__(256, 1) void qgemm_tile_kernel(TileParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // Tile order: each XCD (workgroup id % 8) takes a contiguous run of tiles in M-major
-  // order, so the activation panel it walks N with stays in its L2.
+  // Tile order: each XCD (workgroup id % 8) takes a contiguous run of the launch's
+  // (K split, tile) pairs in split-major, then M-major order, so the activation panels it
+  // walks N with (one per split and tile row) stay in its L2: with K split eight ways over
+  // 32 tiles each XCD holds the panel of one split instead of all eight.
   const int ntiles = p.tiles_m * p.tiles_n;
-  const int split = blockIdx.x / ntiles;
-  const int b = blockIdx.x - split * ntiles;
-  int t = b;
-  if ((ntiles & 7) == 0) t = (b & 7) * (ntiles >> 3) + (b >> 3);
+  const int nb = (int)gridDim.x;
+  const int f = (nb & 7) == 0 ? ((int)blockIdx.x & 7) * (nb >> 3) + ((int)blockIdx.x >> 3) : (int)blockIdx.x;
+  const int split = f / ntiles;
+  const int t = f - split * ntiles;
   const int tm = t / p.tiles_n, tn = t - tm * p.tiles_n;
   // the weight this tile column belongs to (scalar search), its fields selected with
   // static kernel-argument offsets so every load is issued at once
