@@ -190,11 +190,15 @@ __device__ __forceinline__ void word_prelude(const Raw<QT>& r, const Scales<QT>&
     t.a = f16_bits_to_f32(r.d & 0xffffu);
     t.c = QT == QT_Q4_0 ? (MM ? -8.f * t.a : 8.f) : f16_bits_to_f32(r.d >> 16);
   } else if constexpr (QT == QT_Q6_K) {
+    // the six-bit values of the word in the Q4_K byte order (u0: weights 0, 4, 1, 5; u1:
+    // 2, 6, 3, 7): low nibbles from ql, then the two high bits from qh, where after the
+    // shift by 8(kk & 1) weight 2s has its bits at 2s and weight 2s+1 at 16 + 2s
     uint32_t lw = r.ql[kk], hv = r.qh[kk >> 1];
     pin(lw);
     pin(hv);
-    t.u0 = lw;
-    t.u1 = hv;
+    const uint32_t x = (kk & 1) ? (hv >> 8) : hv;
+    t.u0 = (lw & nib) | ((x << 4) & 0x00300030u) | ((x << 8) & 0x30003000u);
+    t.u1 = ((lw >> 4) & nib) | ((x << 2) & 0x00300030u) | ((x << 6) & 0x30003000u);
     t.a = (kk < 2) ? s.a[q] : s.b[q];
     t.c = MM ? -32.f * t.a : 32.f;
   } else {
@@ -225,12 +229,13 @@ __device__ __forceinline__ uint32_t word_quarter(const WordTmp<QT>& t, uint32_t 
                        __builtin_fmaf(t.a, (float)((v >> (16 + sh)) & 0xffu), t.c));
     return pack2<XT>(((float)((v >> sh) & 0xffu) - t.c) * t.a, ((float)((v >> (16 + sh)) & 0xffu) - t.c) * t.a);
   } else if constexpr (QT == QT_Q6_K) {
-    constexpr int rs = 8 * (kk & 1) + 2 * qq - 4;
-    const uint32_t hs = rs >= 0 ? (t.u1 >> rs) : (t.u1 << (-rs));
-    const uint32_t v = ((t.u0 >> (4 * qq)) & (nib & 0x000F000Fu)) | (hs & 0x00300030u);
+    // bytes as Q4_K's (see word_prelude)
+    const uint32_t v = (qq & 1) ? t.u1 : t.u0;
+    const int sh = (qq & 2) ? 8 : 0;
     if constexpr (MM)
-      return pack2<XT>(__builtin_fmaf(t.a, (float)(v & 0xffu), t.c), __builtin_fmaf(t.a, (float)((v >> 16) & 0xffu), t.c));
-    return pack2<XT>(t.a * ((float)(v & 0xffu) - t.c), t.a * ((float)((v >> 16) & 0xffu) - t.c));
+      return pack2<XT>(__builtin_fmaf(t.a, (float)((v >> sh) & 0xffu), t.c),
+                       __builtin_fmaf(t.a, (float)((v >> (16 + sh)) & 0xffu), t.c));
+    return pack2<XT>(t.a * ((float)((v >> sh) & 0xffu) - t.c), t.a * ((float)((v >> (16 + sh)) & 0xffu) - t.c));
   } else {
     // bytes hold q + 128 (sign bits flipped in the prelude)
     const uint32_t v = (qq < 2) ? t.u0 : t.u1;
