@@ -311,9 +311,13 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
   const int M = p.M, N = p.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK16 - 1) / TK16;
-  const int ksplit = blockIdx.x / p.slabs;
+  // each XCD (workgroup id % 8) takes a contiguous run of (K split, slab) pairs, so with K
+  // split it reads the activations of one or two splits, not all of them
+  const int nb = (int)gridDim.x;
+  const int f = (nb & 7) == 0 ? ((int)blockIdx.x & 7) * (nb >> 3) + ((int)blockIdx.x >> 3) : (int)blockIdx.x;
+  const int ksplit = f / p.slabs;
   const bool sw = p.swiglu != 0;
-  const int n0 = (blockIdx.x - ksplit * p.slabs) * (sw ? 16 : 32);
+  const int n0 = (f - ksplit * p.slabs) * (sw ? 16 : 32);
   const int r = lane & 15, j = lane >> 4;
   uint32_t row_sub[RT], row_sb[RT];
   bool rok[RT];
