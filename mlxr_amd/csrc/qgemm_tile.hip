@@ -28,8 +28,9 @@ using namespace tile;
 // the rows); a round of workgroups costs its steps plus 0.8 (prologue, epilogue); a
 // split launch adds the reduce kernel, about 3 us plus its partial-sum traffic at
 // ~5 TB/s (one 256-row step is ~1.86 us).  Splits are whole groups of eight steps (two
-// super-blocks: the kernel's loop runs whole rings of eight steps), at most eight splits,
+// super-blocks: the kernel's loop runs whole rings of eight steps), at most kMaxSplits splits,
 // and only with a workspace of S*M*N*4 bytes.
+constexpr int kMaxSplits = 16;
 struct SplitPlan {
   int bm, tiles, S, kps;
 };
@@ -40,7 +41,7 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
   double best_t = 1e30;
   for (int bm : {256, 128, 64}) {
     const long tiles = ((M + bm - 1) / bm) * tn;
-    for (int S = 1; S <= 8; ++S) {
+    for (int S = 1; S <= kMaxSplits; ++S) {
       const int kps = (((nkt + S - 1) / S) + 7) / 8 * 8;
       const int Sr = (nkt + kps - 1) / kps;  // splits actually used
       if (Sr != S) continue;
