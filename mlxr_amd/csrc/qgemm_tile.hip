@@ -24,13 +24,17 @@ using namespace tile;
 
 
 // Tile rows and K split of a launch, from a small cost model in units of one 256-row
-// tile step: a 128-row tile step costs 0.64 of it (the weight dequant is shared by half
+// tile step: a 128-row tile step costs 0.62 of it (the weight dequant is shared by half
 // the rows); a round of workgroups costs its steps plus 0.8 (prologue, epilogue); a
 // split launch adds the reduce kernel, about 3 us plus its partial-sum traffic at
 // ~5 TB/s (one 256-row step is ~1.86 us).  Splits are whole groups of eight steps (two
 // super-blocks: the kernel's loop runs whole rings of eight steps), at most kMaxSplits splits,
 // and only with a workspace of S*M*N*4 bytes.
 constexpr int kMaxSplits = 16;
+// Cost of one K step of a tile of bm rows, in 256-row steps (measured on MI355X; 0.62 for
+// 128-row tiles ranks Llama-3-70B q,k at M = 256 as measured: three splits of 128-row
+// tiles 62.6 us, six of 256-row tiles 65.3 us).
+constexpr double step_cost(int bm) { return bm == 256 ? 1.0 : bm == 128 ? 0.62 : 0.5; }
 struct SplitPlan {
   int bm, tiles, S, kps;
 };
@@ -47,7 +51,7 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
       if (Sr != S) continue;
       if (S > 1 && (kps < 8 || (size_t)S * (size_t)M * (size_t)N * 4u > ws_bytes)) continue;
       const long rounds = (tiles * S + cus - 1) / cus;
-      double t = (double)rounds * (kps * (bm == 256 ? 1.0 : bm == 128 ? 0.64 : 0.5) + 0.8);
+      double t = (double)rounds * (kps * step_cost(bm) + 0.8);
       if (S > 1) t += (3.0 + (double)S * M * N * 8.0 / 5e6) / 1.86;
       if (t < best_t) {
         best_t = t;
@@ -438,7 +442,7 @@ double mfma_est_us(int M, int N, int K, int qtype, size_t ws_bytes) {
   // Q6_K steps dequantize more per weight: measured on MI355X (Llama-3-70B v, 1024x8192,
   // M = 256) 40.6 us against 24.8 us for the Q4_K weight of the same shape
   const double qf = qtype == QT_Q6_K ? 1.6 : 1.0;
-  double t = (double)rounds * (sp.kps * (sp.bm == 256 ? 1.0 : sp.bm == 128 ? 0.64 : 0.5) * qf + 0.8);
+  double t = (double)rounds * (sp.kps * step_cost(sp.bm) * qf + 0.8);
   if (sp.S > 1) t += (3.0 + (double)sp.S * M * N * 8.0 / 5e6) / 1.86;
   // launches of one ring per workgroup take about 4.5 us more than the model says
   // (measured on MI355X, Llama-3-8B q/k shapes at M = 64-512)
