@@ -84,7 +84,7 @@ def test_block_geometry_and_sizes():
     l = orc.lib()
     assert [l.orc_block_bytes(t) for t in (Q80, Q4K, Q6K)] == [34, 144, 210]
     assert [l.orc_block_elems(t) for t in (Q80, Q4K, Q6K)] == [32, 256, 256]
-    # BASELINE.md byte counts (GGUF sizes of the configuration weights)
+    # GGUF weight byte counts of the benchmark configurations (N·K/256·144 for Q4_K, N·K/32·34 for Q8_0)
     assert l.orc_weight_bytes(Q80, 2048, 2048) == 4456448
     assert l.orc_weight_bytes(Q4K, 4096, 4096) == 9437184
     assert l.orc_weight_bytes(Q4K, 1024, 4096) == 2359296
