@@ -76,3 +76,67 @@ def test_random_call_matches_oracle(cuda, seed):
     # half-precision outputs add their own rounding (2^-9 / 2^-12 relative) to the contract
     assert orc.rel_err(yh, ref) <= TOL, label
     assert orc.normwise_rel_err(yh, exact) <= TOL, label
+
+
+@pytest.mark.parametrize("seed", list(range(40)))
+def test_random_grouped_call_matches_oracle(cuda, seed):
+    """One to five weights sharing X (random types and N, so some share a launch and some
+    run alone), with or without the workspace the library asks for: every output against
+    the oracle as above, and the call repeated gives the same bits."""
+    import torch
+    rng = np.random.default_rng(5000 + seed)
+    kq = bool(rng.integers(2))
+    K = 256 * int(rng.integers(1, 9)) if kq else 32 * int(rng.integers(1, 65))
+    pool = TYPES[:3] if kq else TYPES[3:]
+    n = int(rng.integers(1, 6))
+    specs = [(pool[int(rng.integers(len(pool)))], int(rng.integers(1, 600))) for _ in range(n)]
+    M = int(rng.choice([1, 2, 4, 8, 33, 64, 100, 256, 300]))
+    use_ws = bool(rng.integers(2))
+    gg = [mx.synth_gguf(qt, N, K, 6000 + 16 * seed + i) for i, (qt, N) in enumerate(specs)]
+    pws = [mx.pack_weights(g, N, K, qt, device=cuda) for g, (qt, N) in zip(gg, specs)]
+    bits = mx.synth_act(M * K, mx.BF16, 7000 + seed)
+    x = torch.from_numpy(bits.view(np.int16).reshape(M, K)).to(cuda).view(torch.bfloat16)
+    xf = orc.bf16_bits_to_f32(bits).reshape(M, K)
+    ys = mx.q_gemm_dequant_grouped(x, pws, out_dtype=torch.float32, workspace=use_ws)
+    ys2 = mx.q_gemm_dequant_grouped(x, pws, out_dtype=torch.float32, workspace=use_ws)
+    torch.cuda.synchronize()
+    for i, ((qt, N), y, y2) in enumerate(zip(specs, ys, ys2)):
+        label = (i, str(qt), M, N, K, use_ws)
+        assert torch.equal(y, y2), label
+        yh = y.cpu().numpy()
+        exact = orc.gemm_f64(int(qt), M, N, K, gg[i], xf)
+        ref = exact if M <= 4 else orc.gemm_f64(int(qt), M, N, K, gg[i], xf, w_to_bf16=True)
+        assert orc.rel_err(yh, ref) <= TOL, label
+        assert orc.normwise_rel_err(yh, exact) <= TOL, label
+
+
+@pytest.mark.parametrize("seed", list(range(32)))
+def test_random_swiglu_matches_oracle(cuda, seed):
+    """The fused gate/up/gating entry at random M (the GEMV, skinny and tiled kernels), type,
+    N and K, with and without its workspace: h against swish(g) * u of the oracle's g and u
+    (over the operands each kernel multiplies)."""
+    import torch
+    rng = np.random.default_rng(8000 + seed)
+    qt = TYPES[int(rng.integers(len(TYPES)))]
+    blk = mx.get_default_group_size(qt)
+    K = blk * int(rng.integers(1, 2048 // blk + 1)) if blk == 256 else 32 * int(rng.integers(1, 65))
+    N = int(rng.integers(1, 600))
+    M = int(rng.choice([1, 3, 4, 5, 8, 16, 31, 32, 33, 64, 100, 256]))
+    use_ws = bool(rng.integers(2))
+    wg = mx.synth_gguf(qt, N, K, 9000 + seed)
+    wu = mx.synth_gguf(qt, N, K, 9500 + seed)
+    pg = mx.pack_weights(wg, N, K, qt, device=cuda)
+    pu = mx.pack_weights(wu, N, K, qt, device=cuda)
+    bits = mx.synth_act(M * K, mx.BF16, 9900 + seed)
+    x = torch.from_numpy(bits.view(np.int16).reshape(M, K)).to(cuda).view(torch.bfloat16)
+    xf = orc.bf16_bits_to_f32(bits).reshape(M, K)
+    h = mx.q_gemm_swiglu(x, pg, pu, out_dtype=torch.float32, workspace=use_ws)
+    h2 = mx.q_gemm_swiglu(x, pg, pu, out_dtype=torch.float32, workspace=use_ws)
+    torch.cuda.synchronize()
+    label = (str(qt), M, N, K, use_ws)
+    assert torch.equal(h, h2), label
+    rb = M > 4
+    g = orc.gemm_f64(int(qt), M, N, K, wg, xf, w_to_bf16=rb).astype(np.float64)
+    u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=rb).astype(np.float64)
+    ref = g / (1.0 + np.exp(-g)) * u
+    assert orc.rel_err(h.cpu().numpy(), ref) <= TOL, label
