@@ -258,10 +258,14 @@ int mlxr_qgemm_mlp_status(void* workspace_dev, void* stream);
  * by tests to exercise the timeout path.  mlxr_qgemm_test_force_skinny(1): every call of the
  * MFMA family (M > 4, or MLXR_PATH_MFMA) runs the skinny kernel, at any M, until called
  * with 0; tests use it to reach the skinny kernel's 64-row M blocks at shapes the automatic
- * choice gives to the tiled kernel.  All are process-wide (atomics). */
+ * choice gives to the tiled kernel.  mlxr_qgemm_test_skinny_stage(0): the narrow skinny
+ * kernel reads its activations from global memory at every step instead of staging them in
+ * LDS once (its mode at M <= 8 when a wavefront's share fits; 1 restores it); tests use it to
+ * check both modes against the oracle.  All are process-wide (atomics). */
 int mlxr_qgemm_test_set_operand_limit(size_t bytes);
 int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks);
 int mlxr_qgemm_test_force_skinny(int on);
+int mlxr_qgemm_test_skinny_stage(int on);
 
 /* Deterministic synthetic inputs with the shapes/distributions of the benchmark
  * configurations (host memory).  Generator: SplitMix64 from `seed`; normals by

@@ -666,6 +666,11 @@ int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks) {
   return MLXR_OK;
 }
 
+int mlxr_qgemm_test_skinny_stage(int on) {
+  mlxr::g_skinny_stage.store(on ? 1 : 0, std::memory_order_relaxed);
+  return MLXR_OK;
+}
+
 int mlxr_qgemm_test_force_skinny(int on) {
   g_force_skinny.store(on ? 1 : 0, std::memory_order_relaxed);
   return MLXR_OK;

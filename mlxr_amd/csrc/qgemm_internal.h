@@ -2,6 +2,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "qgemm_layout.h"
 
 namespace mlxr {
@@ -75,6 +77,9 @@ size_t device_lds_limit();
 // Skinny MFMA GEMM for M <= 64 (qgemm_skinny.hip), weights streamed once.  With a.ws,
 // shapes with fewer 32-row slabs than CUs also split K over workgroups.
 hipError_t launch_skinny(const RunArgs& a, hipStream_t s);
+// Whether the narrow skinny kernel stages its activations in LDS where they fit (default 1;
+// test hook mlxr_qgemm_test_skinny_stage).
+extern std::atomic<int> g_skinny_stage;
 // Whether every operand of a is below operand_limit() (else: launch_mfma, which chunks).
 bool skinny_fits(const RunArgs& a);
 // Workspace bytes launch_skinny would use (0: no split).

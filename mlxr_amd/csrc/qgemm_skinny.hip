@@ -21,6 +21,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -30,6 +31,8 @@
 #include "qgemm_wdequant.h"
 
 namespace mlxr {
+
+std::atomic<int> g_skinny_stage{1};
 
 namespace {
 
@@ -298,13 +301,22 @@ __device__ __forceinline__ void decode_hdr16(const Hdr<QT>& h, int j, Scales<QT>
   }
 }
 
-template <int QT, int XT, int NB>
+// Staged-activation mode (XL): at M <= 8 a wavefront's activations for its whole K range fit
+// in XL_LOADS 16-byte loads per lane; they are read once into LDS, so the K loop's only
+// global loads are the weights.
+constexpr int XL_LOADS = 16;
+
+template <int QT, int XT, int NB, bool XL = false>
 __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams p) {
+  static_assert(!XL || NB == 1, "staged activations cover one 16-row block");
   constexpr int D = ring16_steps<QT>();  // raw ring; loads run D - 1 steps ahead
   constexpr int RT = 2;                  // 16-row weight tiles per wavefront
   constexpr bool KQ = is_kquant(QT);
   constexpr int XD = 2;                  // activation loads run two steps ahead
-  __shared__ f32x4_t red[MAXW][RT * NB][64];
+  // XL: the dynamic LDS holds the wavefronts' activation stages, then the reduction
+  __shared__ f32x4_t red_s[XL ? 1 : MAXW][RT * NB][64];
+  extern __shared__ __attribute__((aligned(16))) uint8_t xl_lds[];
+  f32x4_t(*const red)[RT * NB][64] = XL ? reinterpret_cast<f32x4_t(*)[RT * NB][64]>(xl_lds) : red_s;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nw = blockDim.x >> 6;
@@ -345,9 +357,26 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
     const int m = nb * 16 + r;
     xoff[nb] = m < M ? ((uint32_t)m * (uint32_t)K + 32u * (uint32_t)j) * 2u : OOB;
   }
-  u32x4_t xf[4][4][NB];  // step s in slot s % 4 (three live: loads run two steps ahead)
+  u32x4_t xf[XL ? 2 : 4][4][NB];  // step s in slot s % 4 (three live: loads run two steps ahead)
+  // XL stage of this wavefront: step s (from kt0), row m at (s*M + m) * 256 bytes, its 16-byte
+  // chunk c (K 8c .. 8c+7 of the step) at position c ^ m, so the 16 rows that one MFMA operand
+  // read takes from chunk column c land in 16 different bank groups.  Lanes of rows >= M read
+  // row M - 1: those lanes only feed output rows that are never stored.
+  uint8_t* const xs = xl_lds + (size_t)wave * (size_t)p.spw * (size_t)M * 256u;
+  uint32_t xl_off[4];
+  if constexpr (XL) {
+    const int rr = min(r, M - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) xl_off[kk] = (uint32_t)rr * 256u + (uint32_t)(((4 * j + kk) ^ rr) << 4);
+  }
   auto load_x = [&](int kt, auto SLOT) {
     constexpr int slot = decltype(SLOT)::value;
+    if constexpr (XL) {
+      const uint8_t* b = xs + (size_t)(kt - kt0) * (size_t)M * 256u;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) xf[slot & 1][kk][0] = *(const u32x4_t*)(b + xl_off[kk]);
+      return;
+    }
     const bool live = kt < kt1 && 4 * kt + j < nsub;
     const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane(kt * TK16 * 2);
 #pragma unroll
@@ -379,22 +408,55 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[t][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  sfor<D - 1>([&](auto S_) {
-    constexpr int s_ = decltype(S_)::value;
-    issue_raw(kt0 + s_, std::integral_constant<int, s_>());
-    if constexpr (s_ < XD) load_x(kt0 + s_, std::integral_constant<int, s_>());
-  });
-  sfor<(XD > D - 1 ? XD - D + 1 : 0)>([&](auto S_) {
-    constexpr int s_ = decltype(S_)::value + D - 1;
-    load_x(kt0 + s_, std::integral_constant<int, s_>());
-  });
+  if constexpr (XL) {
+    // the whole stage (spw steps, zeros past kt1 and past K) is read before the weight ring
+    // is issued, then written to LDS while the ring is in flight
+    const int per = M * 4;  // 64-byte row quarters per step
+    const uint32_t minv = (65536u + (uint32_t)per - 1u) / (uint32_t)per;  // exact g / per for g < 256
+    u32x4_t st[XL_LOADS];
+    uint32_t dst[XL_LOADS];
+#pragma unroll
+    for (int i = 0; i < XL_LOADS; ++i) {
+      const int g = i * 16 + (lane >> 2);  // (step, row, quarter) of this lane's 16 bytes
+      const int s = (int)(((uint32_t)g * minv) >> 16), rem = g - s * per;
+      const int m = rem >> 2, c = 4 * (rem & 3) + (lane & 3);
+      const int kt = kt0 + s;
+      const bool ok = s < p.spw && kt < kt1 && 4 * kt + (c >> 2) < nsub;
+      const uint32_t vo = ok ? ((uint32_t)m * (uint32_t)K + (uint32_t)kt * TK16 + 8u * (uint32_t)c) * 2u : OOB;
+      st[i] = __builtin_amdgcn_raw_buffer_load_b128(RX, vo, 0, 0);
+      dst[i] = s < p.spw ? (uint32_t)(s * M + m) * 256u + (uint32_t)((c ^ m) << 4) : ~0u;
+    }
+    sfor<D - 1>([&](auto S_) {
+      constexpr int s_ = decltype(S_)::value;
+      issue_raw(kt0 + s_, std::integral_constant<int, s_>());
+    });
+#pragma unroll
+    for (int i = 0; i < XL_LOADS; ++i)
+      if (dst[i] != ~0u) *(u32x4_t*)(xs + dst[i]) = st[i];
+    load_x(kt0, std::integral_constant<int, 0>());
+  } else {
+    sfor<D - 1>([&](auto S_) {
+      constexpr int s_ = decltype(S_)::value;
+      issue_raw(kt0 + s_, std::integral_constant<int, s_>());
+      if constexpr (s_ < XD) load_x(kt0 + s_, std::integral_constant<int, s_>());
+    });
+    sfor<(XD > D - 1 ? XD - D + 1 : 0)>([&](auto S_) {
+      constexpr int s_ = decltype(S_)::value + D - 1;
+      load_x(kt0 + s_, std::integral_constant<int, s_>());
+    });
+  }
   // Step kt = kt0 + D*i + u (kt0 even, so an even u starts a super-block) issues the raw
   // loads of step kt + D - 1, then the activations of step kt + 2: the wait for the
   // activations of step kt (in-order counter) then covers raw loads issued two steps ago.
   auto step = [&](int kt, auto U) {
     constexpr int u = decltype(U)::value;
     issue_raw(kt + D - 1, std::integral_constant<int, (u + D - 1) % D>());
-    load_x(kt + XD, std::integral_constant<int, (u + XD) & 3>());
+    // XL: the LDS read of the next step, while it lies inside this wavefront's stage
+    if constexpr (XL) {
+      if (kt + 1 < kt0 + p.spw) load_x(kt + 1, std::integral_constant<int, (u + 1) & 1>());
+    } else {
+      load_x(kt + XD, std::integral_constant<int, (u + XD) & 3>());
+    }
     constexpr int ru = u % D;
     if constexpr (KQ && (u & 1) == 0) {
 #pragma unroll
@@ -410,7 +472,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[t][nb] = mfma16<XT>(w[kk], xf[u & 3][kk][nb], acc[t][nb]);
+        for (int nb = 0; nb < NB; ++nb) acc[t][nb] = mfma16<XT>(w[kk], xf[XL ? (u & 1) : (u & 3)][kk][nb], acc[t][nb]);
     }
   };
   for (int kt = kt0; kt < kt1; kt += UNROLL16) {
@@ -422,6 +484,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
 
   // Accumulator tile (t, nb): lane holds Y[m][n .. n+3] for m = nb*16 + lane%16,
   // n = n0 + 16t + 4(lane/16) (SwiGLU: n = n0 + 4(lane/16) of weight t).
+  if constexpr (XL) __syncthreads();  // the reduction reuses the activation stages
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
@@ -548,6 +611,10 @@ SkinnyPlan skinny16_plan(int N, int K, bool allow_split, int unroll, int wcap, i
 
 bool use_skinny16(int M) { return M <= 32; }
 
+// Staged activations at most this many bytes per workgroup: two workgroups (eight
+// wavefronts, the register-bound occupancy) still fit in a CU's 160 KiB of LDS.
+constexpr size_t kXlMaxBytes = 64u * 1024u;
+
 // The narrow kernel's plan: SwiGLU slabs are 16 rows of two weights, planned as 32-row
 // slabs of a problem with as many slabs.
 SkinnyPlan s16_plan(const SkinnyParams& sp, bool allow_split) {
@@ -572,7 +639,28 @@ hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   const void* const bias = sp.bias;
   if (pl.ks == 1) sp.ws = nullptr;
   const dim3 grid((unsigned)(sp.slabs * pl.ks)), block((unsigned)(64 * pl.w));
-  if (sp.M <= 16) {
+  // Staged activations: only where a wavefront runs at least eight steps (shorter ranges
+  // lose more to the staging latency than the K loop gains) and the stages do not limit how
+  // many workgroups a CU holds at once.  Same products in the same order either way.
+  const size_t xl_bytes = (size_t)pl.w * (size_t)pl.spw * (size_t)sp.M * 256u;
+  // the stages, or the reduction of the wavefronts' partial tiles if larger
+  const size_t lds = std::max(xl_bytes, (size_t)pl.w * 2u * 64u * 16u);
+  const bool stage = g_skinny_stage.load(std::memory_order_relaxed) && sp.M <= 8 && pl.spw >= 8 &&
+                     pl.spw * sp.M * 4 <= XL_LOADS * 16 && lds <= kXlMaxBytes &&
+                     (long)(device_lds_limit() / lds) * device_cu_count() >= (long)grid.x;
+  if (stage) {
+    static std::atomic<uint64_t> attr_set{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+      const hipError_t e = hipFuncSetAttribute((const void*)qgemm_skinny16_kernel<QT, XT, 1, true>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXlMaxBytes);
+      if (e != hipSuccess) return e;
+      attr_set.fetch_or(bit, std::memory_order_release);
+    }
+    qgemm_skinny16_kernel<QT, XT, 1, true><<<grid, block, lds, s>>>(sp);
+  } else if (sp.M <= 16) {
     qgemm_skinny16_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
   } else {
     qgemm_skinny16_kernel<QT, XT, 2><<<grid, block, 0, s>>>(sp);

@@ -87,6 +87,7 @@ _SIGS = {
     "mlxr_qgemm_test_set_operand_limit": (ctypes.c_int, [ctypes.c_size_t]),
     "mlxr_qgemm_test_set_mlp_spin_limit": (ctypes.c_int, [ctypes.c_uint]),
     "mlxr_qgemm_test_force_skinny": (ctypes.c_int, [ctypes.c_int]),
+    "mlxr_qgemm_test_skinny_stage": (ctypes.c_int, [ctypes.c_int]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
 }
@@ -432,3 +433,9 @@ def test_force_skinny(on):
     """Test hook: send every MFMA-family call to the skinny kernel (any M, in 64-row blocks
     of M above 32) while on."""
     _check(lib().mlxr_qgemm_test_force_skinny(1 if on else 0))
+
+
+def test_skinny_stage(on):
+    """Test hook: whether the narrow skinny kernel stages its activations in LDS where they
+    fit (on by default); off, it reads them from global memory at every step."""
+    _check(lib().mlxr_qgemm_test_skinny_stage(1 if on else 0))

@@ -480,6 +480,62 @@ def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
     assert err <= 3e-5, err
 
 
+# Shapes whose narrow-kernel plan stages the activations in LDS (M <= 8, eight or more steps
+# per wavefront): Llama-3-8B gate, ragged N with a bias and half-precision outputs, K not a
+# multiple of the 128-wide step (Q4_0, Q8_0), M <= 4 through the MFMA path.
+@pytest.mark.parametrize("qt,M,N,K,path,ydt", [(Q4K, 8, 14336, 4096, mx.PATH_AUTO, "f32"),
+                                               (Q6K, 6, 14000, 4096, mx.PATH_AUTO, "bf16"),
+                                               (Q80, 5, 11008, 4000, mx.PATH_AUTO, "f16"),
+                                               (Q40, 7, 13000, 4064, mx.PATH_AUTO, "f32"),
+                                               (Q5K, 1, 14336, 4096, mx.PATH_MFMA, "f32"),
+                                               (Q41, 3, 11000, 4096, mx.PATH_MFMA, "bf16")])
+def test_skinny_staged_activations_match_oracle(cuda, qt, M, N, K, path, ydt):
+    """The narrow skinny kernel with its activations staged in LDS gives the same bits as the
+    kernel reading them from global memory (same products in the same order), and both
+    agree with the oracle over the bf16-rounded weights."""
+    import torch
+    w, pw = _packed(torch, qt, N, K, 211 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 221 + M, cuda)
+    bias = torch.linspace(-1, 1, N, device=cuda).to(torch.bfloat16)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[ydt]
+    ys = {}
+    try:
+        for on in (True, False):
+            mx.qgemm.test_skinny_stage(on)
+            ys[on] = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=tdt, path=path)
+    finally:
+        mx.qgemm.test_skinny_stage(True)
+    torch.cuda.synchronize()
+    assert torch.equal(ys[True], ys[False])
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bias.float().cpu().numpy(), w_to_bf16=True)
+    # half-precision outputs add their own rounding (2^-9 / 2^-12 relative)
+    assert orc.rel_err(ys[True].float().cpu().numpy(), ref) <= (5e-3 if ydt != "f32" else 3e-5)
+
+
+@pytest.mark.parametrize("M", [6, 8])
+def test_skinny_staged_swiglu_matches_oracle(cuda, M):
+    """Fused SwiGLU through the staged narrow kernel (16-row slabs of gate and up, 512 of
+    them: N = 8192 at K = 4096): same bits as the global-read mode, and the oracle's
+    swish(g) * u within 5e-3."""
+    import torch
+    qt, N, K = Q4K, 8192, 4096
+    wg, pg = _packed(torch, qt, N, K, 231, cuda)
+    wu, pu = _packed(torch, qt, N, K, 232, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 233 + M, cuda)
+    hs = {}
+    try:
+        for on in (True, False):
+            mx.qgemm.test_skinny_stage(on)
+            hs[on] = mx.q_gemm_swiglu(x, pg, pu, out_dtype=torch.float32)
+    finally:
+        mx.qgemm.test_skinny_stage(True)
+    torch.cuda.synchronize()
+    assert torch.equal(hs[True], hs[False])
+    g = orc.gemm_f64(int(qt), M, N, K, wg, xf, w_to_bf16=True).astype(np.float64)
+    u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=True).astype(np.float64)
+    assert orc.rel_err(hs[True].cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= 5e-3
+
+
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 1024, 4096), (Q6K, 4096, 4096)])
 def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda, qt, N, K):
     """Shapes at M = 128 whose estimated times favour the skinny kernel: Llama-3-8B k (the
