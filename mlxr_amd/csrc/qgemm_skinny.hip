@@ -611,9 +611,10 @@ SkinnyPlan skinny16_plan(int N, int K, bool allow_split, int unroll, int wcap, i
 
 bool use_skinny16(int M) { return M <= 32; }
 
-// Staged activations at most this many bytes per workgroup: two workgroups (eight
-// wavefronts, the register-bound occupancy) still fit in a CU's 160 KiB of LDS.
-constexpr size_t kXlMaxBytes = 64u * 1024u;
+// Staged activations at most this many bytes per workgroup (with the reduction's static
+// LDS, within a CU's 160 KiB); the launcher also requires that the whole grid still fits on
+// the device at the workgroups per CU the stages leave.
+constexpr size_t kXlMaxBytes = 128u * 1024u;
 
 // The narrow kernel's plan: SwiGLU slabs are 16 rows of two weights, planned as 32-row
 // slabs of a problem with as many slabs.

@@ -482,13 +482,16 @@ def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
 
 # Shapes whose narrow-kernel plan stages the activations in LDS (M <= 8, eight or more steps
 # per wavefront): Llama-3-8B gate, ragged N with a bias and half-precision outputs, K not a
-# multiple of the 128-wide step (Q4_0, Q8_0), M <= 4 through the MFMA path.
+# multiple of the 128-wide step (Q4_0, Q8_0), M <= 4 through the MFMA path, down shapes (K
+# split over two workgroups, seven wavefronts of 112 KiB of stages).
 @pytest.mark.parametrize("qt,M,N,K,path,ydt", [(Q4K, 8, 14336, 4096, mx.PATH_AUTO, "f32"),
                                                (Q6K, 6, 14000, 4096, mx.PATH_AUTO, "bf16"),
                                                (Q80, 5, 11008, 4000, mx.PATH_AUTO, "f16"),
                                                (Q40, 7, 13000, 4064, mx.PATH_AUTO, "f32"),
                                                (Q5K, 1, 14336, 4096, mx.PATH_MFMA, "f32"),
-                                               (Q41, 3, 11000, 4096, mx.PATH_MFMA, "bf16")])
+                                               (Q41, 3, 11000, 4096, mx.PATH_MFMA, "bf16"),
+                                               (Q80, 8, 4096, 14336, mx.PATH_AUTO, "f32"),
+                                               (Q6K, 7, 4000, 14336, mx.PATH_AUTO, "bf16")])
 def test_skinny_staged_activations_match_oracle(cuda, qt, M, N, K, path, ydt):
     """The narrow skinny kernel with its activations staged in LDS gives the same bits as the
     kernel reading them from global memory (same products in the same order), and both
