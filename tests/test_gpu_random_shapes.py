@@ -140,3 +140,40 @@ def test_random_swiglu_matches_oracle(cuda, seed):
     u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=rb).astype(np.float64)
     ref = g / (1.0 + np.exp(-g)) * u
     assert orc.rel_err(h.cpu().numpy(), ref) <= TOL, label
+
+
+@pytest.mark.parametrize("seed", list(range(16)))
+def test_random_staged_skinny_call_matches_oracle(cuda, seed):
+    """Random shapes in the range where the narrow skinny kernel stages its activations in
+    LDS (M <= 8 through the MFMA path, thousands of rows, K of 4096 or a little less or more):
+    the staged call gives the same bits as the global-read one, and both are within the
+    contract of the oracle over the bf16-rounded weights."""
+    import torch
+    rng = np.random.default_rng(12000 + seed)
+    qt = TYPES[int(rng.integers(len(TYPES)))]
+    blk = mx.get_default_group_size(qt)
+    K = 4096 + blk * int(rng.integers(-2, 3))
+    M = int(rng.integers(1, 9))
+    N = int(rng.integers(6000, 16000))
+    use_bias = bool(rng.integers(2))
+    ydt = str(rng.choice(["bf16", "f16", "f32"]))
+    w = mx.synth_gguf(qt, N, K, 13000 + seed)
+    pw = mx.pack_weights(w, N, K, qt, device=cuda)
+    bits = mx.synth_act(M * K, mx.BF16, 14000 + seed)
+    x = torch.from_numpy(bits.view(np.int16).reshape(M, K)).to(cuda).view(torch.bfloat16)
+    xf = orc.bf16_bits_to_f32(bits).reshape(M, K)
+    bias = torch.linspace(-1, 1, N, device=cuda).to(torch.bfloat16) if use_bias else None
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[ydt]
+    ys = {}
+    try:
+        for on in (True, False):
+            mx.qgemm.test_skinny_stage(on)
+            ys[on] = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=tdt, path=mx.PATH_MFMA)
+    finally:
+        mx.qgemm.test_skinny_stage(True)
+    torch.cuda.synchronize()
+    label = (str(qt), M, N, K, use_bias, ydt)
+    assert torch.equal(ys[True], ys[False]), label
+    bf = bias.float().cpu().numpy() if bias is not None else None
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bf, w_to_bf16=True)
+    assert orc.rel_err(ys[True].float().cpu().numpy(), ref) <= TOL, label
