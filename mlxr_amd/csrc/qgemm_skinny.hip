@@ -615,6 +615,8 @@ bool use_skinny16(int M) { return M <= 32; }
 // LDS, within a CU's 160 KiB); the launcher also requires that the whole grid still fits on
 // the device at the workgroups per CU the stages leave.
 constexpr size_t kXlMaxBytes = 128u * 1024u;
+// Static LDS of the staged kernel (its unused reduction array of one wavefront).
+constexpr size_t kXlStaticBytes = 2u * 64u * 16u;
 
 // The narrow kernel's plan: SwiGLU slabs are 16 rows of two weights, planned as 32-row
 // slabs of a problem with as many slabs.
@@ -648,7 +650,7 @@ hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   const size_t lds = std::max(xl_bytes, (size_t)pl.w * 2u * 64u * 16u);
   const bool stage = g_skinny_stage.load(std::memory_order_relaxed) && sp.M <= 8 && pl.spw >= 8 &&
                      pl.spw * sp.M * 4 <= XL_LOADS * 16 && lds <= kXlMaxBytes &&
-                     (long)(device_lds_limit() / lds) * device_cu_count() >= (long)grid.x;
+                     (long)(device_lds_limit() / (lds + kXlStaticBytes)) * device_cu_count() >= (long)grid.x;
   if (stage) {
     static std::atomic<uint64_t> attr_set{0};
     int dev = 0;
