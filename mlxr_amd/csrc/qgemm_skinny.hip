@@ -17,7 +17,8 @@
 // (32 rows of N), the activations the second (32 rows of M, twice for M > 32), read from
 // global memory (they are small and stay in L2).  Raw weights are loaded seven steps
 // ahead, activations two, as branch-free buffer loads.  At the end the W partial tiles
-// meet in LDS and are added in wavefront order.
+// meet in LDS and are added in wavefront order.  (The narrow variant at M <= 8 can instead
+// stage a wavefront's activations in LDS once, before its K loop: see XL below.)
 #include <stdlib.h>
 
 #include <algorithm>
