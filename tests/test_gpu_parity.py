@@ -483,7 +483,8 @@ def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
 # Shapes whose narrow-kernel plan stages the activations in LDS (M <= 8, eight or more steps
 # per wavefront): Llama-3-8B gate, ragged N with a bias and half-precision outputs, K not a
 # multiple of the 128-wide step (Q4_0, Q8_0), M <= 4 through the MFMA path, down shapes (K
-# split over two workgroups, seven wavefronts of 112 KiB of stages).
+# split over two workgroups, seven wavefronts of 112 KiB of stages), long stages at M = 1
+# and 2 (32 and 16 steps per wavefront).
 @pytest.mark.parametrize("qt,M,N,K,path,ydt", [(Q4K, 8, 14336, 4096, mx.PATH_AUTO, "f32"),
                                                (Q6K, 6, 14000, 4096, mx.PATH_AUTO, "bf16"),
                                                (Q80, 5, 11008, 4000, mx.PATH_AUTO, "f16"),
@@ -491,7 +492,9 @@ def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
                                                (Q5K, 1, 14336, 4096, mx.PATH_MFMA, "f32"),
                                                (Q41, 3, 11000, 4096, mx.PATH_MFMA, "bf16"),
                                                (Q80, 8, 4096, 14336, mx.PATH_AUTO, "f32"),
-                                               (Q6K, 7, 4000, 14336, mx.PATH_AUTO, "bf16")])
+                                               (Q6K, 7, 4000, 14336, mx.PATH_AUTO, "bf16"),
+                                               (Q4K, 1, 9000, 32768, mx.PATH_MFMA, "f32"),
+                                               (Q40, 2, 9000, 16384, mx.PATH_MFMA, "f32")])
 def test_skinny_staged_activations_match_oracle(cuda, qt, M, N, K, path, ydt):
     """The narrow skinny kernel with its activations staged in LDS gives the same bits as the
     kernel reading them from global memory (same products in the same order), and both
