@@ -518,6 +518,28 @@ def test_skinny_staged_activations_match_oracle(cuda, qt, M, N, K, path, ydt):
     assert orc.rel_err(ys[True].float().cpu().numpy(), ref) <= (5e-3 if ydt != "f32" else 3e-5)
 
 
+@pytest.mark.parametrize("qt,M", [(Q4K, 8), (Q80, 5), (Q6K, 3)])
+def test_skinny_staged_f16_activations_match_oracle(cuda, qt, M):
+    """fp16 activations (the fp16 MFMA, fp16-rounded weights) through the staged narrow
+    kernel on the Llama-3-8B gate shape: same bits as the global-read mode, within 3e-5 of
+    the oracle over the fp16-rounded weights."""
+    import torch
+    N, K = 14336, 4096
+    w, pw = _packed(torch, qt, N, K, 281 + M, cuda)
+    x, xf = _act(torch, M, K, mx.F16, 291 + M, cuda)
+    ys = {}
+    try:
+        for on in (True, False):
+            mx.qgemm.test_skinny_stage(on)
+            ys[on] = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    finally:
+        mx.qgemm.test_skinny_stage(True)
+    torch.cuda.synchronize()
+    assert torch.equal(ys[True], ys[False])
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_f16=True)
+    assert orc.rel_err(ys[True].cpu().numpy(), ref) <= 3e-5
+
+
 @pytest.mark.parametrize("M", [6, 8])
 def test_skinny_staged_swiglu_matches_oracle(cuda, M):
     """Fused SwiGLU through the staged narrow kernel (16-row slabs of gate and up, 512 of
