@@ -177,3 +177,53 @@ def test_random_staged_skinny_call_matches_oracle(cuda, seed):
     bf = bias.float().cpu().numpy() if bias is not None else None
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bf, w_to_bf16=True)
     assert orc.rel_err(ys[True].float().cpu().numpy(), ref) <= TOL, label
+
+
+@pytest.mark.parametrize("chunk", list(range(8)))
+def test_random_calls_against_dequantized_weights(cuda, chunk):
+    """50 seeded random calls per chunk, wider than the oracle cases (M to 600, N to 15000,
+    K to 16384, fp16 activations, workspaces of random bytes or one byte short of the size
+    asked for): each against an fp64 product over the library's own dequantized weights
+    (bit-exact to the oracle by the dequant tests; rounded to the activation type where an
+    MFMA kernel consumes them), within the 5e-3 contract, and bit-identical on repeat."""
+    import torch
+    fails = []
+    for it in range(50 * chunk, 50 * chunk + 50):
+        rng = np.random.default_rng(20000 + it)
+        qt = TYPES[int(rng.integers(len(TYPES)))]
+        blk = mx.get_default_group_size(qt)
+        K = blk * int(rng.integers(1, (16384 if rng.random() < 0.2 else 4096) // blk + 1))
+        M = int(rng.choice([1, 2, 4, 5, 7, 8, 9, 16, 17, 31, 32, 33, 48, 64, 65, 128, 200, 256, 300, 600]))
+        N = int(rng.integers(1, 3000)) if rng.random() < 0.7 else int(rng.integers(3000, 15000))
+        path = int(rng.choice([mx.PATH_AUTO, mx.PATH_AUTO, mx.PATH_MFMA] + ([mx.PATH_GEMV] if M <= 64 else [])))
+        xdt = mx.BF16 if rng.random() < 0.8 else mx.F16
+        ydt = int(rng.choice([mx.BF16, mx.F16, mx.F32]))
+        wsmode = int(rng.integers(3))  # none, the size asked for (random bytes), one byte short
+        pw = mx.pack_weights(mx.synth_gguf(qt, N, K, 30000 + it), N, K, qt, device=cuda)
+        g = torch.Generator(device=cuda).manual_seed(40000 + it)
+        x = (torch.randn(M, K, device=cuda, generator=g) * 0.7).to(torch.bfloat16 if xdt == mx.BF16 else torch.float16)
+        bias = torch.randn(N, device=cuda, generator=g).to(torch.bfloat16) if rng.random() < 0.5 else None
+        need = mx.workspace_size(qt, N, K, M)
+        nb = 0 if wsmode == 0 or need == 0 else (need if wsmode == 1 else need - 1)
+        ws = torch.randint(0, 256, (max(nb, 1),), dtype=torch.uint8, device=cuda, generator=g)
+        tdt = {mx.BF16: torch.bfloat16, mx.F16: torch.float16, mx.F32: torch.float32}[ydt]
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        ys = []
+        for _ in range(2):
+            y = torch.empty((M, N), dtype=tdt, device=cuda)
+            rc = mx.lib().mlxr_qgemm_run_ws(int(qt), N, K, 0, pw.data_ptr(), x.data_ptr(), xdt,
+                                            bias.data_ptr() if bias is not None else None, mx.BF16, y.data_ptr(),
+                                            ydt, M, path, ws.data_ptr() if nb else None, nb, s)
+            assert rc == 0, (mx.lib().mlxr_qgemm_last_error(), it)
+            ys.append(y)
+        wd = mx.dequantize(pw, torch.float32)
+        if not (path == mx.PATH_GEMV or (path == mx.PATH_AUTO and M <= 4)):
+            wd = wd.to(x.dtype).float()
+        ref = x.double() @ wd.double().T
+        if bias is not None:
+            ref += bias.double()
+        err = ((ys[0].double() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+        label = (it, str(qt), M, N, K, path, xdt, ydt, wsmode, bias is not None)
+        if not torch.equal(ys[0], ys[1]) or not err <= TOL:
+            fails.append((label, err))
+    assert not fails, fails
