@@ -658,8 +658,11 @@ hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+      // the most this kernel ever asks for, within what the device allows (the launch
+      // condition above keeps every launch below both)
+      const size_t cap = std::min(kXlMaxBytes, device_lds_limit() - kXlStaticBytes);
       const hipError_t e = hipFuncSetAttribute((const void*)qgemm_skinny16_kernel<QT, XT, 1, true>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXlMaxBytes);
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)cap);
       if (e != hipSuccess) return e;
       attr_set.fetch_or(bit, std::memory_order_release);
     }
