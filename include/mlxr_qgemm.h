@@ -260,8 +260,9 @@ int mlxr_qgemm_mlp_status(void* workspace_dev, void* stream);
  * with 0; tests use it to reach the skinny kernel's 64-row M blocks at shapes the automatic
  * choice gives to the tiled kernel.  mlxr_qgemm_test_skinny_stage(0): the narrow skinny
  * kernel reads its activations from global memory at every step instead of staging them in
- * LDS once (its mode at M <= 8 when a wavefront's share fits; 1 restores it); tests use it to
- * check both modes against the oracle.  All are process-wide (atomics). */
+ * LDS once (its mode at M <= 16 when the stages fit; 1 restores it; 2 prefers the mode where
+ * two slabs share their stages wherever it fits); tests use it to check every mode against
+ * the oracle.  All are process-wide (atomics). */
 int mlxr_qgemm_test_set_operand_limit(size_t bytes);
 int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks);
 int mlxr_qgemm_test_force_skinny(int on);

@@ -667,7 +667,7 @@ int mlxr_qgemm_test_set_mlp_spin_limit(unsigned ticks) {
 }
 
 int mlxr_qgemm_test_skinny_stage(int on) {
-  mlxr::g_skinny_stage.store(on ? 1 : 0, std::memory_order_relaxed);
+  mlxr::g_skinny_stage.store(on <= 0 ? 0 : on >= 2 ? 2 : 1, std::memory_order_relaxed);
   return MLXR_OK;
 }
 

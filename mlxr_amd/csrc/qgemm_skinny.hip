@@ -302,14 +302,17 @@ __device__ __forceinline__ void decode_hdr16(const Hdr<QT>& h, int j, Scales<QT>
   }
 }
 
-// Staged-activation mode (XL): at M <= 8 a wavefront's activations for its whole K range fit
-// in XL_LOADS 16-byte loads per lane; they are read once into LDS, so the K loop's only
-// global loads are the weights.
+// Staged-activation mode (XL): a wavefront's activations for its whole K range (at most
+// XL_LOADS 16-byte loads per lane) are read once into LDS, so the K loop's only global loads
+// are the weights.  SP = 2: a workgroup holds two slabs (SwiGLU: two 16-row slab pairs), the
+// wavefronts of both walking the same K ranges, so each stage serves two wavefronts (half
+// the LDS per slab, and the two share its loads).
 constexpr int XL_LOADS = 16;
 
-template <int QT, int XT, int NB, bool XL = false>
+template <int QT, int XT, int NB, bool XL = false, int SP = 1>
 __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams p) {
   static_assert(!XL || NB == 1, "staged activations cover one 16-row block");
+  static_assert(SP == 1 || (SP == 2 && XL), "paired slabs share a stage");
   constexpr int D = ring16_steps<QT>();  // raw ring; loads run D - 1 steps ahead
   constexpr int RT = 2;                  // 16-row weight tiles per wavefront
   constexpr bool KQ = is_kquant(QT);
@@ -321,6 +324,8 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nw = blockDim.x >> 6;
+  // wavefront roles: slab sg of the workgroup's SP, K range wk of the slab's W
+  const int W = nw / SP, sg = wave / W, wk = wave - sg * W;
   const int M = p.M, N = p.N, K = p.K;
   const int nsub = K >> 5, nsb = K >> 8;
   const int nkt = (K + TK16 - 1) / TK16;
@@ -328,9 +333,12 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
   // split it reads the activations of one or two splits, not all of them
   const int nb = (int)gridDim.x;
   const int f = (nb & 7) == 0 ? ((int)blockIdx.x & 7) * (nb >> 3) + ((int)blockIdx.x >> 3) : (int)blockIdx.x;
-  const int ksplit = f / p.slabs;
+  const int gpk = (p.slabs + SP - 1) / SP;  // workgroups per K split
+  const int ksplit = f / gpk;
   const bool sw = p.swiglu != 0;
-  const int n0 = (f - ksplit * p.slabs) * (sw ? 16 : 32);
+  // (SP = 2 with an odd slab count: the last workgroup's second slab lies past N, its rows
+  // read zeros and store nothing)
+  const int n0 = ((f - ksplit * gpk) * SP + sg) * (sw ? 16 : 32);
   const int r = lane & 15, j = lane >> 4;
   uint32_t row_sub[RT], row_sb[RT];
   bool rok[RT];
@@ -342,7 +350,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
     row_sb[t] = rok[t] ? (uint32_t)n * (uint32_t)nsb : 0u;
   }
   const int kg1 = min(nkt, (ksplit + 1) * p.spg);
-  const int kt0 = ksplit * p.spg + wave * p.spw, kt1 = min(kg1, kt0 + p.spw);
+  const int kt0 = ksplit * p.spg + wk * p.spw, kt1 = min(kg1, kt0 + p.spw);
   rsrc_t R[RT][4];  // row tile t's weight (SwiGLU: tile 1 reads the up weight)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -363,7 +371,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
   // chunk c (K 8c .. 8c+7 of the step) at position c ^ m, so the 16 rows that one MFMA operand
   // read takes from chunk column c land in 16 different bank groups.  Lanes of rows >= M read
   // row M - 1: those lanes only feed output rows that are never stored.
-  uint8_t* const xs = xl_lds + (size_t)wave * (size_t)p.spw * (size_t)M * 256u;
+  uint8_t* const xs = xl_lds + (size_t)wk * (size_t)p.spw * (size_t)M * 256u;
   uint32_t xl_off[4];
   if constexpr (XL) {
     const int rr = min(r, M - 1);
@@ -413,12 +421,14 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
     // the whole stage (spw steps, zeros past kt1 and past K) is read before the weight ring
     // is issued, then written to LDS while the ring is in flight
     const int per = M * 4;  // 64-byte row quarters per step
-    const uint32_t minv = (65536u + (uint32_t)per - 1u) / (uint32_t)per;  // exact g / per for g < 256
+    const uint32_t minv = (65536u + (uint32_t)per - 1u) / (uint32_t)per;  // exact g / per for g < 512
     u32x4_t st[XL_LOADS];
     uint32_t dst[XL_LOADS];
 #pragma unroll
     for (int i = 0; i < XL_LOADS; ++i) {
-      const int g = i * 16 + (lane >> 2);  // (step, row, quarter) of this lane's 16 bytes
+      // (step, row, quarter) of this lane's 16 bytes; the SP wavefronts sharing the stage
+      // take interleaved load rounds
+      const int g = (i * SP + sg) * 16 + (lane >> 2);
       const int s = (int)(((uint32_t)g * minv) >> 16), rem = g - s * per;
       const int m = rem >> 2, c = 4 * (rem & 3) + (lane & 3);
       const int kt = kt0 + s;
@@ -434,6 +444,7 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
 #pragma unroll
     for (int i = 0; i < XL_LOADS; ++i)
       if (dst[i] != ~0u) *(u32x4_t*)(xs + dst[i]) = st[i];
+    if constexpr (SP > 1) __syncthreads();  // the stage holds the other wavefront's share too
     load_x(kt0, std::integral_constant<int, 0>());
   } else {
     sfor<D - 1>([&](auto S_) {
@@ -492,14 +503,16 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
     for (int nb = 0; nb < NB; ++nb) red[wave][t * NB + nb][lane] = acc[t][nb];
   __syncthreads();
   if (sw) {
-    // wavefront w finishes M-blocks w, w + nw, ...: gate and up sums of the same outputs
-    for (int nb = wave; nb < NB; nb += nw) {
+    // wavefront wk of slab sg finishes M-blocks wk, wk + W, ...: gate and up sums of the
+    // same outputs, over the slab's wavefronts in order
+    for (int nb = wk; nb < NB; nb += W) {
       const int m = nb * 16 + r;
       if (m >= M) continue;
-      f32x4_t g = red[0][nb][lane], u = red[0][NB + nb][lane];
-      for (int w = 1; w < nw; ++w) {
-        g += red[w][nb][lane];
-        u += red[w][NB + nb][lane];
+      const int w0 = sg * W;
+      f32x4_t g = red[w0][nb][lane], u = red[w0][NB + nb][lane];
+      for (int w = 1; w < W; ++w) {
+        g += red[w0 + w][nb][lane];
+        u += red[w0 + w][NB + nb][lane];
       }
       const int nn = n0 + 4 * j;
       if (p.ws) {  // K split over workgroups: partial sums, gate then up columns
@@ -527,12 +540,13 @@ __global__ __launch_bounds__(64 * MAXW) void qgemm_skinny16_kernel(SkinnyParams 
     }
     return;
   }
-  for (int u = wave; u < RT * NB; u += nw) {
+  for (int u = wk; u < RT * NB; u += W) {
     const int t = u / NB, nb = u - t * NB;
     const int m = nb * 16 + r;
     if (m >= M) continue;
-    f32x4_t sum = red[0][u][lane];
-    for (int w = 1; w < nw; ++w) sum += red[w][u][lane];
+    const int w0 = sg * W;
+    f32x4_t sum = red[w0][u][lane];
+    for (int w = 1; w < W; ++w) sum += red[w0 + w][u][lane];
     const int nn = n0 + 16 * t + 4 * j;
     const size_t rowbase = (size_t)m * N;
     if (p.ws) {  // K split over workgroups: this split's fp32 partial sums, no bias
@@ -645,28 +659,63 @@ hipError_t launch_s16(SkinnyParams sp, size_t ws_bytes, hipStream_t s) {
   const dim3 grid((unsigned)(sp.slabs * pl.ks)), block((unsigned)(64 * pl.w));
   // Staged activations: only where a wavefront runs at least eight steps (shorter ranges
   // lose more to the staging latency than the K loop gains) and the stages do not limit how
-  // many workgroups a CU holds at once.  Same products in the same order either way.
-  const size_t xl_bytes = (size_t)pl.w * (size_t)pl.spw * (size_t)sp.M * 256u;
-  // the stages, or the reduction of the wavefronts' partial tiles if larger
-  const size_t lds = std::max(xl_bytes, (size_t)pl.w * 2u * 64u * 16u);
-  const bool stage = g_skinny_stage.load(std::memory_order_relaxed) && sp.M <= 8 && pl.spw >= 8 &&
-                     pl.spw * sp.M * 4 <= XL_LOADS * 16 && lds <= kXlMaxBytes &&
-                     (long)(device_lds_limit() / (lds + kXlStaticBytes)) * device_cu_count() >= (long)grid.x;
-  if (stage) {
-    static std::atomic<uint64_t> attr_set{0};
+  // many workgroups a CU holds at once; one slab per workgroup where that fits, else two
+  // slabs sharing their stages (half the LDS per slab).  Same products in the same order
+  // in every mode.
+  const int mode = g_skinny_stage.load(std::memory_order_relaxed);  // 0 off, 2: paired first
+  // wavefronts per SIMD the staged kernels' registers allow, queried once per device
+  static std::atomic<int> occ_cache[2][64];
+  auto simd_occupancy = [&](int sps) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+    int v = occ_cache[sps - 1][dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+      const void* fn = sps == 1 ? (const void*)qgemm_skinny16_kernel<QT, XT, 1, true, 1>
+                                : (const void*)qgemm_skinny16_kernel<QT, XT, 1, true, 2>;
+      int nb = 0;  // resident four-wavefront workgroups without dynamic LDS: one wave per SIMD each
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 256, 0) != hipSuccess || nb <= 0) nb = 1;
+      v = nb;
+      occ_cache[sps - 1][dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+  };
+  auto stage_fits = [&](int sps, size_t* lds) {
+    const long groups = (long)(sp.slabs + sps - 1) / sps * pl.ks;
+    const size_t xl_bytes = (size_t)pl.w * (size_t)pl.spw * (size_t)sp.M * 256u;
+    // the stages, or the reduction of the wavefronts' partial tiles if larger
+    *lds = std::max(xl_bytes, (size_t)sps * pl.w * 2u * 64u * 16u);
+    if (!(sp.M <= 8 * sps && pl.w * sps <= MAXW && pl.spw >= 8 && pl.spw * sp.M * 4 <= sps * XL_LOADS * 16 &&
+          *lds <= kXlMaxBytes))
+      return false;
+    // the whole grid resident at once: workgroups per CU by LDS, and by registers (a
+    // workgroup of more than four wavefronts puts two or more on a SIMD; measured on MI355X,
+    // grids past this ran a second round and lost to the global-read mode)
+    const long by_lds = (long)(device_lds_limit() / (*lds + kXlStaticBytes));
+    const long by_regs = simd_occupancy(sps) / ((pl.w * sps + 3) / 4);
+    return std::min(by_lds, by_regs) * device_cu_count() >= groups;
+  };
+  size_t lds1 = 0, lds2 = 0;
+  const bool fit1 = mode != 0 && stage_fits(1, &lds1), fit2 = mode != 0 && stage_fits(2, &lds2);
+  const int sps = fit1 && !(mode == 2 && fit2) ? 1 : fit2 ? 2 : 0;
+  if (sps) {
+    const size_t lds = sps == 1 ? lds1 : lds2;
+    const dim3 sgrid((unsigned)((sp.slabs + sps - 1) / sps * pl.ks)), sblock((unsigned)(64 * pl.w * sps));
+    const void* const fn = sps == 1 ? (const void*)qgemm_skinny16_kernel<QT, XT, 1, true, 1>
+                                    : (const void*)qgemm_skinny16_kernel<QT, XT, 1, true, 2>;
+    static std::atomic<uint64_t> attr_set[2];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     const uint64_t bit = 1ull << (dev & 63);
-    if (!(attr_set.load(std::memory_order_acquire) & bit)) {
+    if (!(attr_set[sps - 1].load(std::memory_order_acquire) & bit)) {
       // the most this kernel ever asks for, within what the device allows (the launch
       // condition above keeps every launch below both)
       const size_t cap = std::min(kXlMaxBytes, device_lds_limit() - kXlStaticBytes);
-      const hipError_t e = hipFuncSetAttribute((const void*)qgemm_skinny16_kernel<QT, XT, 1, true>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)cap);
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)cap);
       if (e != hipSuccess) return e;
-      attr_set.fetch_or(bit, std::memory_order_release);
+      attr_set[sps - 1].fetch_or(bit, std::memory_order_release);
     }
-    qgemm_skinny16_kernel<QT, XT, 1, true><<<grid, block, lds, s>>>(sp);
+    if (sps == 1) qgemm_skinny16_kernel<QT, XT, 1, true, 1><<<sgrid, sblock, lds, s>>>(sp);
+    else qgemm_skinny16_kernel<QT, XT, 1, true, 2><<<sgrid, sblock, lds, s>>>(sp);
   } else if (sp.M <= 16) {
     qgemm_skinny16_kernel<QT, XT, 1><<<grid, block, 0, s>>>(sp);
   } else {

@@ -435,7 +435,8 @@ def test_force_skinny(on):
     _check(lib().mlxr_qgemm_test_force_skinny(1 if on else 0))
 
 
-def test_skinny_stage(on):
+def test_skinny_stage(mode):
     """Test hook: whether the narrow skinny kernel stages its activations in LDS where they
-    fit (on by default); off, it reads them from global memory at every step."""
-    _check(lib().mlxr_qgemm_test_skinny_stage(1 if on else 0))
+    fit (True / 1, the default); False / 0: it reads them from global memory at every step;
+    2: two slabs per workgroup share their stages wherever that fits."""
+    _check(lib().mlxr_qgemm_test_skinny_stage(int(mode)))

@@ -484,7 +484,8 @@ def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
 # per wavefront): Llama-3-8B gate, ragged N with a bias and half-precision outputs, K not a
 # multiple of the 128-wide step (Q4_0, Q8_0), M <= 4 through the MFMA path, down shapes (K
 # split over two workgroups, seven wavefronts of 112 KiB of stages), long stages at M = 1
-# and 2 (32 and 16 steps per wavefront).
+# and 2 (32 and 16 steps per wavefront), M = 9 to 16 (two slabs per workgroup sharing their
+# stages; 14300 rows: an odd slab count, the last workgroup's second slab past N).
 @pytest.mark.parametrize("qt,M,N,K,path,ydt", [(Q4K, 8, 14336, 4096, mx.PATH_AUTO, "f32"),
                                                (Q6K, 6, 14000, 4096, mx.PATH_AUTO, "bf16"),
                                                (Q80, 5, 11008, 4000, mx.PATH_AUTO, "f16"),
@@ -494,11 +495,18 @@ def test_skinny_m_blocks_match_oracle(cuda, qt, M, N, K):
                                                (Q80, 8, 4096, 14336, mx.PATH_AUTO, "f32"),
                                                (Q6K, 7, 4000, 14336, mx.PATH_AUTO, "bf16"),
                                                (Q4K, 1, 9000, 32768, mx.PATH_MFMA, "f32"),
-                                               (Q40, 2, 9000, 16384, mx.PATH_MFMA, "f32")])
+                                               (Q40, 2, 9000, 16384, mx.PATH_MFMA, "f32"),
+                                               (Q4K, 16, 14336, 4096, mx.PATH_AUTO, "bf16"),
+                                               (Q80, 12, 14000, 4000, mx.PATH_AUTO, "f32"),
+                                               (Q6K, 9, 4096, 14336, mx.PATH_AUTO, "f16"),
+                                               (Q41, 13, 11001, 4096, mx.PATH_AUTO, "f32"),
+                                               (Q4K, 12, 14300, 4096, mx.PATH_AUTO, "bf16")])
 def test_skinny_staged_activations_match_oracle(cuda, qt, M, N, K, path, ydt):
-    """The narrow skinny kernel with its activations staged in LDS gives the same bits as the
-    kernel reading them from global memory (same products in the same order), and both
-    agree with the oracle over the bf16-rounded weights."""
+    """The narrow skinny kernel with its activations staged in LDS (one slab per workgroup
+    where that fits, two slabs sharing their stages otherwise or when preferred through the
+    test hook) gives the same bits as the kernel reading them from global memory (same
+    products in the same order), and all agree with the oracle over the bf16-rounded
+    weights."""
     import torch
     w, pw = _packed(torch, qt, N, K, 211 + M, cuda)
     x, xf = _act(torch, M, K, mx.BF16, 221 + M, cuda)
@@ -506,16 +514,17 @@ def test_skinny_staged_activations_match_oracle(cuda, qt, M, N, K, path, ydt):
     tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[ydt]
     ys = {}
     try:
-        for on in (True, False):
-            mx.qgemm.test_skinny_stage(on)
-            ys[on] = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=tdt, path=path)
+        for mode in (1, 2, 0):
+            mx.qgemm.test_skinny_stage(mode)
+            ys[mode] = mx.q_gemm_dequant(x, pw, M, N, K, qt, bias=bias, out_dtype=tdt, path=path)
     finally:
-        mx.qgemm.test_skinny_stage(True)
+        mx.qgemm.test_skinny_stage(1)
     torch.cuda.synchronize()
-    assert torch.equal(ys[True], ys[False])
+    assert torch.equal(ys[1], ys[0])
+    assert torch.equal(ys[2], ys[0])
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bias.float().cpu().numpy(), w_to_bf16=True)
     # half-precision outputs add their own rounding (2^-9 / 2^-12 relative)
-    assert orc.rel_err(ys[True].float().cpu().numpy(), ref) <= (5e-3 if ydt != "f32" else 3e-5)
+    assert orc.rel_err(ys[1].float().cpu().numpy(), ref) <= (5e-3 if ydt != "f32" else 3e-5)
 
 
 @pytest.mark.parametrize("qt,M", [(Q4K, 8), (Q80, 5), (Q6K, 3)])
@@ -540,7 +549,7 @@ def test_skinny_staged_f16_activations_match_oracle(cuda, qt, M):
     assert orc.rel_err(ys[True].cpu().numpy(), ref) <= 3e-5
 
 
-@pytest.mark.parametrize("M", [6, 8])
+@pytest.mark.parametrize("M", [6, 8, 16])
 def test_skinny_staged_swiglu_matches_oracle(cuda, M):
     """Fused SwiGLU through the staged narrow kernel (16-row slabs of gate and up, 512 of
     them: N = 8192 at K = 4096): same bits as the global-read mode, and the oracle's
@@ -552,16 +561,17 @@ def test_skinny_staged_swiglu_matches_oracle(cuda, M):
     x, xf = _act(torch, M, K, mx.BF16, 233 + M, cuda)
     hs = {}
     try:
-        for on in (True, False):
-            mx.qgemm.test_skinny_stage(on)
-            hs[on] = mx.q_gemm_swiglu(x, pg, pu, out_dtype=torch.float32)
+        for mode in (1, 2, 0):
+            mx.qgemm.test_skinny_stage(mode)
+            hs[mode] = mx.q_gemm_swiglu(x, pg, pu, out_dtype=torch.float32)
     finally:
-        mx.qgemm.test_skinny_stage(True)
+        mx.qgemm.test_skinny_stage(1)
     torch.cuda.synchronize()
-    assert torch.equal(hs[True], hs[False])
+    assert torch.equal(hs[1], hs[0])
+    assert torch.equal(hs[2], hs[0])
     g = orc.gemm_f64(int(qt), M, N, K, wg, xf, w_to_bf16=True).astype(np.float64)
     u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=True).astype(np.float64)
-    assert orc.rel_err(hs[True].cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= 5e-3
+    assert orc.rel_err(hs[1].cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= 5e-3
 
 
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 1024, 4096), (Q6K, 4096, 4096)])
