@@ -65,6 +65,56 @@ SplitPlan plan_split(int M, int N, int K, size_t ws_bytes) {
 }
 
 
+// The reduce kernels issue every load of a thread before its first add: up to eight
+// splits' partials at a time and the bias values, so a thread waits for memory about once
+// instead of once per split and once per bias value (a loop that adds as it loads waits for
+// each load in turn).  The sums run in split order as before.
+template <int VEC>
+__device__ __forceinline__ void load_vec(const float* q, float* out) {
+  if constexpr (VEC == 4) {
+    const float4 a = *(const float4*)q;
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  } else {
+    out[0] = *q;
+  }
+}
+// `then` runs after the first eight splits' loads are issued (the caller's bias loads go
+// there, so they share the first wait).
+template <int VEC, typename Then>
+__device__ __forceinline__ void sum_splits(const float* __restrict__ ws, size_t split_elems, int S, size_t i,
+                                           float* v, Then&& then) {
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    float q[8][VEC];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (s0 + k < S) load_vec<VEC>(ws + (size_t)(s0 + k) * split_elems + i, q[k]);
+    if (s0 == 0) then();
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (s0 + k < S) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = s0 + k == 0 ? q[k][e] : v[e] + q[k][e];
+      }
+  }
+}
+// VEC consecutive bias values as fp32 (0 without a bias); one dtype branch for all of them.
+template <int VEC>
+__device__ __forceinline__ void load_bias(const void* b, int dtype, int n, float* out) {
+  if (!b) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[e] = 0.f;
+  } else if (dtype == DT_F32) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[e] = ((const float*)b)[n + e];
+  } else if (dtype == DT_F16) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[e] = f16_bits_to_f32(((const uint16_t*)b)[n + e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[e] = bf16_bits_to_f32(((const uint16_t*)b)[n + e]);
+  }
+}
+
 // y = sum over splits (in split order) + bias, converted to y's dtype.  VEC consecutive
 // elements per thread (VEC = 4 needs N % 4 == 0).
 template <int VEC>
@@ -73,22 +123,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                                                             int N, size_t total) {
   const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
   if (i >= total) return;
-  float v[VEC];
-  if constexpr (VEC == 4) {
-    const float4 a = *(const float4*)(ws + i);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    for (int sp = 1; sp < S; ++sp) {
-      const float4 b = *(const float4*)(ws + (size_t)sp * split_elems + i);
-      v[0] += b.x; v[1] += b.y; v[2] += b.z; v[3] += b.w;
-    }
-  } else {
-    v[0] = ws[i];
-    for (int sp = 1; sp < S; ++sp) v[0] += ws[(size_t)sp * split_elems + i];
-  }
   const int n = (int)(i % (size_t)N);
+  float bv[VEC], v[VEC];
+  sum_splits<VEC>(ws, split_elems, S, i, v, [&] { load_bias<VEC>(bias, bias_dtype, n, bv); });
   if (bias) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) v[e] += load_scalar(bias, bias_dtype, n + e);
+    for (int e = 0; e < VEC; ++e) v[e] += bv[e];
   }
   if constexpr (VEC == 4) {
     if (y_dtype == DT_F32) {
@@ -117,27 +157,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_grouped_kernel(const float*
                                                                     int S, int ws_ld, size_t total, ReduceGroups rg) {
   const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
   if (i >= total) return;
-  float v[VEC];
-  if constexpr (VEC == 4) {
-    const float4 a = *(const float4*)(ws + i);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    for (int sp = 1; sp < S; ++sp) {
-      const float4 b = *(const float4*)(ws + (size_t)sp * split_elems + i);
-      v[0] += b.x; v[1] += b.y; v[2] += b.z; v[3] += b.w;
-    }
-  } else {
-    v[0] = ws[i];
-    for (int sp = 1; sp < S; ++sp) v[0] += ws[(size_t)sp * split_elems + i];
-  }
   const int m = (int)(i / (size_t)ws_ld), c = (int)(i - (size_t)m * ws_ld);
   int g = 0;
 #pragma unroll
   for (int k = 1; k < MAX_TG; ++k)
     if (k < rg.ngroups && c >= rg.col0[k]) g = k;
   const int n = c - rg.col0[g];
+  float bv[VEC], v[VEC];
+  sum_splits<VEC>(ws, split_elems, S, i, v, [&] { load_bias<VEC>(rg.bias[g], rg.bias_dtype[g], n, bv); });
   if (rg.bias[g]) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) v[e] += load_scalar(rg.bias[g], rg.bias_dtype[g], n + e);
+    for (int e = 0; e < VEC; ++e) v[e] += bv[e];
   }
   const size_t o = (size_t)m * rg.N[g] + n;
   if constexpr (VEC == 4) {
@@ -164,13 +194,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_swiglu_kernel(const float* 
   if (i >= total) return;
   const size_t m = i / (size_t)N, n = i - m * (size_t)N;
   const size_t gi = m * 2 * (size_t)N + n, ui = gi + (size_t)N;
-  float g = ws[gi], u = ws[ui];
-  for (int sp = 1; sp < S; ++sp) {
-    g += ws[(size_t)sp * split_elems + gi];
-    u += ws[(size_t)sp * split_elems + ui];
-  }
-  if (bias_g) g += load_scalar(bias_g, bias_dtype, n);
-  if (bias_u) u += load_scalar(bias_u, bias_dtype, n);
+  float bg, bu, g, u;
+  sum_splits<1>(ws, split_elems, S, gi, &g, [&] { load_bias<1>(bias_g, bias_dtype, (int)n, &bg); });
+  sum_splits<1>(ws, split_elems, S, ui, &u, [&] { load_bias<1>(bias_u, bias_dtype, (int)n, &bu); });
+  if (bias_g) g += bg;
+  if (bias_u) u += bu;
   store_scalar(y, y_dtype, i, swiglu1(g, u));
 }
 
