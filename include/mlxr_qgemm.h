@@ -62,8 +62,9 @@ enum {
 
 /* Execution path selector for mlxr_qgemm_run_ex. */
 enum {
-  MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M <= 4; MFMA kernels above: skinny (weights
-                         streamed once) for M <= 64, tiled GEMM beyond.  When
+  MLXR_PATH_AUTO = 0, /* GEMV (no MFMA) for M = 1 and, depending on the shape
+                         (mlxr_qgemm_auto_path), M <= 4; MFMA kernels above: skinny
+                         (weights streamed once) for M <= 64, tiled GEMM beyond.  When
                          mlxr_qgemm_run_ws is given the workspace it asks for, calls with
                          32 < M <= 256 take whichever of the two is estimated faster for
                          the shape (the skinny one for narrow weights) */
@@ -135,6 +136,13 @@ int mlxr_qgemm_run_ex(int qtype, int N, int K, int group_size, const void* packe
  * When the size is 0 the call makes the same choice with or without a workspace.
  * No counterpart in the reference (its kernel has no K split, q_gemm_dequant.metal:374-464). */
 int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes);
+
+/* The kernel family MLXR_PATH_AUTO runs an [M, N, K] call on: MLXR_PATH_GEMV or
+ * MLXR_PATH_MFMA in *path.  M = 1 is always the GEMV; 2 <= M <= 4 the GEMV unless the rows
+ * are long (K >= 8192 at M >= 3, K >= 16384 at M = 2) or, at M = 4, the weight is large (N*K
+ * >= 48 Mi elements, not Q6_K), where the skinny MFMA kernel is faster; M > 4 the MFMA
+ * kernels.  No counterpart in the reference (its operator has one kernel). */
+int mlxr_qgemm_auto_path(int qtype, int N, int K, int M, int* path);
 
 /* mlxr_qgemm_run_ex with a caller-owned device workspace (workspace_bytes bytes; NULL or
  * too small = the kernel and result of mlxr_qgemm_run_ex).  The workspace must not be

@@ -20,6 +20,22 @@ namespace {
 
 // Largest M the automatic path sends to the GEMV kernel.
 constexpr int kGemvMaxM = 4;
+// Whether the automatic path runs a call with M <= kGemvMaxM on the GEMV kernel.  The GEMV
+// stages all M rows of X per workgroup (M = 3, 4 as four rows), so long rows cost it LDS
+// and occupancy; the skinny MFMA kernel's time hardly depends on M.  Measured on MI355X
+// (µs, GEMV / skinny MFMA without a K split): Llama-3-8B down (4096 x 14336) at M = 3 and
+// 4: 22.1 / 21.3 and 24.9 / 21.8 (the skinny one splits K with a workspace: about 17.5);
+// gate (14336 x 4096) at M = 4 16.5 / 15.1 and at M = 3 14.5 / 14.9; Llama-3-70B down (8192
+// x 28672) at M = 2 51.2 / 38.9; 4096 x 4096 at M = 4 7.4 / 9.8; the Q6_K lm_head (128256 x
+// 4096) at M = 4 116 / 146.
+bool gemv_auto(int M, const mlxr::PackedLayout& L) {
+  if (M <= 1) return true;
+  if (M > kGemvMaxM) return false;
+  if (M >= 3 && L.K >= 8192) return false;
+  if (M == 2 && L.K >= 16384) return false;
+  if (M == 4 && (long)L.N * (long)L.K >= (48L << 20) && L.qtype != mlxr::QT_Q6_K) return false;
+  return true;
+}
 // Up to this M the skinny kernel serves every MFMA call (measured on MI355X, Llama-3-8B
 // FFN shapes: at M = 32 its 16x16x32 variant is ahead of the tiled GEMM with 64-row tiles
 // and split-K, gate 26.9 vs 29.0 us and down 26.7 vs 29.7 us; at M = 64 the tiled one,
@@ -229,8 +245,18 @@ int mlxr_qgemm_workspace_size(int qtype, int N, int K, int M, size_t* bytes) {
     mid_workspace(M, L, bytes);
   else
     *bytes = M > skinny_only_max_m() ? mlxr::mfma_workspace_bytes(M, N, K)
-             : M > kGemvMaxM         ? mlxr::skinny_workspace_bytes(M, N, K, qtype)
+             : !gemv_auto(M, L)      ? mlxr::skinny_workspace_bytes(M, N, K, qtype)
                                      : 0;
+  return MLXR_OK;
+}
+
+int mlxr_qgemm_auto_path(int qtype, int N, int K, int M, int* path) {
+  mlxr::PackedLayout L;
+  const int rc = check_type_shape(qtype, N, K, &L);
+  if (rc) return rc;
+  if (!path) return fail(MLXR_E_INVALID, "null output pointer");
+  if (M < 0) return fail(MLXR_E_INVALID, "Input shape must be [M, K] (M=%d)", M);
+  *path = gemv_auto(M, L) ? MLXR_PATH_GEMV : MLXR_PATH_MFMA;
   return MLXR_OK;
 }
 
@@ -270,10 +296,10 @@ int mlxr_qgemm_run_ws(int qtype, int N, int K, int group_size, const void* packe
   a.M = M;
   a.ws = workspace_dev;
   a.ws_bytes = workspace_dev ? workspace_bytes : 0;
-  // GEMV (no MFMA) for decode; MFMA kernels otherwise: the skinny one up to M = 32, then up
-  // to M = 256 the skinny or the tiled one (skinny_mid), the tiled one above
+  // GEMV (no MFMA) for decode (gemv_auto); MFMA kernels otherwise: the skinny one up to
+  // M = 32, then up to M = 256 the skinny or the tiled one (skinny_mid), the tiled one above
   // (MLXR_PATH_GEMV / MLXR_PATH_MFMA force the family)
-  const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && M <= kGemvMaxM);
+  const bool gemv = path == MLXR_PATH_GEMV || (path == MLXR_PATH_AUTO && gemv_auto(M, a.L));
   // the skinny kernels address operands with 32-bit offsets; the tiled launcher splits
   // larger problems into chunks
   bool skinny = false;

@@ -88,6 +88,8 @@ _SIGS = {
     "mlxr_qgemm_test_set_mlp_spin_limit": (ctypes.c_int, [ctypes.c_uint]),
     "mlxr_qgemm_test_force_skinny": (ctypes.c_int, [ctypes.c_int]),
     "mlxr_qgemm_test_skinny_stage": (ctypes.c_int, [ctypes.c_int]),
+    "mlxr_qgemm_auto_path": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.POINTER(ctypes.c_int)]),
     "mlxr_synth_gguf": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
     "mlxr_synth_act": (ctypes.c_int, [ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p]),
 }
@@ -292,6 +294,13 @@ def q_gemm_dequant(input, weights, M, N, K, quant_type, group_size=0, bias=None,
                                    _dt_code(out.dtype), M, path, ws.data_ptr() if ws is not None else None,
                                    ws_bytes, _stream_ptr(stream)))
     return out
+
+
+def auto_path(qtype, N, K, M):
+    """The kernel family PATH_AUTO runs an [M, N, K] call on: PATH_GEMV or PATH_MFMA."""
+    v = ctypes.c_int(0)
+    _check(lib().mlxr_qgemm_auto_path(int(qtype), N, K, M, ctypes.byref(v)))
+    return v.value
 
 
 def workspace_size(qtype, N, K, M):

@@ -178,7 +178,26 @@ def test_workspace_sizes_hold_whole_partial_planes():
             for M in [1, 4, 5, 8, 16, 32, 33, 64, 65, 100, 128, 200, 256, 257, 512, 2048]:
                 w = mx.workspace_size(qt, N, K, M)
                 assert w == mx.workspace_size(qt, N, K, M)
-                if M <= 4:
+                if M <= 4 and mx.auto_path(qt, N, K, M) == mx.PATH_GEMV:
                     assert w == 0, (qt, N, K, M, w)
                 assert w % (4 * M * N) == 0, (qt, N, K, M, w)
                 assert w == 0 or w // (4 * M * N) >= 2, (qt, N, K, M, w)
+
+
+def test_auto_path_rule():
+    """The automatic path's kernel family: the GEMV at M = 1 and for short rows at M <= 4;
+    the skinny MFMA kernel for long rows at M = 3, 4 (K >= 8192) and M = 2 (K >= 16384) and
+    for large weights at M = 4 (not Q6_K); MFMA above M = 4.  A call the MFMA kernels take
+    at M <= 4 gets a workspace size when its slabs are few (down shapes)."""
+    Q4K, Q6K = int(mx.QuantType.Q4_K), int(mx.QuantType.Q6_K)
+    G, F = mx.PATH_GEMV, mx.PATH_MFMA
+    cases = [(Q4K, 14336, 4096, 1, G), (Q4K, 4096, 14336, 1, G), (Q4K, 8192, 28672, 1, G),
+             (Q4K, 4096, 14336, 2, G), (Q4K, 8192, 28672, 2, F), (Q4K, 4096, 4096, 3, G),
+             (Q4K, 4096, 14336, 3, F), (Q4K, 14336, 4096, 3, G), (Q4K, 14336, 4096, 4, F),
+             (Q4K, 4096, 4096, 4, G), (Q6K, 128256, 4096, 4, G), (Q6K, 4096, 14336, 4, F),
+             (Q4K, 100, 256, 5, F), (Q4K, 100, 256, 0, G)]
+    for qt, N, K, M, want in cases:
+        assert mx.auto_path(qt, N, K, M) == want, (qt, N, K, M)
+    assert mx.workspace_size(Q4K, 4096, 14336, 3) > 0
+    assert mx.workspace_size(Q4K, 4096, 14336, 2) == 0
+

@@ -574,6 +574,24 @@ def test_skinny_staged_swiglu_matches_oracle(cuda, M):
     assert orc.rel_err(hs[1].cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= 5e-3
 
 
+@pytest.mark.parametrize("qt,M,N,K", [(Q4K, 3, 4096, 14336), (Q6K, 4, 2000, 8192), (Q4K, 2, 1500, 16384),
+                                      (Q80, 4, 14336, 4096)])
+def test_auto_path_takes_mfma_for_long_rows_at_small_m(cuda, qt, M, N, K):
+    """At M <= 4 the automatic path runs long rows (and, at M = 4, large weights) on the skinny
+    MFMA kernel: the same bits as the forced MFMA path with the workspace the library asks
+    for, within the contract of the oracle over the bf16-rounded weights."""
+    import torch
+    assert mx.auto_path(qt, N, K, M) == mx.PATH_MFMA
+    w, pw = _packed(torch, qt, N, K, 301 + M, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 311 + M, cuda)
+    y_auto = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32)
+    y_mfma = mx.q_gemm_dequant(x, pw, M, N, K, qt, out_dtype=torch.float32, path=mx.PATH_MFMA)
+    torch.cuda.synchronize()
+    assert torch.equal(y_auto, y_mfma)
+    ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
+    assert orc.rel_err(y_auto.cpu().numpy(), ref) <= 3e-5
+
+
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 1024, 4096), (Q6K, 4096, 4096)])
 def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda, qt, N, K):
     """Shapes at M = 128 whose estimated times favour the skinny kernel: Llama-3-8B k (the

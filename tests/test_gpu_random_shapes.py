@@ -64,7 +64,7 @@ def test_random_call_matches_oracle(cuda, seed):
     y1, y2 = run(), run()
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
-    gemv = path == mx.PATH_GEMV or (path == mx.PATH_AUTO and M <= 4)
+    gemv = path == mx.PATH_GEMV or (path == mx.PATH_AUTO and mx.auto_path(qt, N, K, M) == mx.PATH_GEMV)
     bf = bias.float().cpu().numpy() if bias is not None else None
     yh = y1.float().cpu().numpy()
     exact = orc.gemm_f64(int(qt), M, N, K, w, xf, bias=bf)
@@ -217,7 +217,7 @@ def test_random_calls_against_dequantized_weights(cuda, chunk):
             assert rc == 0, (mx.lib().mlxr_qgemm_last_error(), it)
             ys.append(y)
         wd = mx.dequantize(pw, torch.float32)
-        if not (path == mx.PATH_GEMV or (path == mx.PATH_AUTO and M <= 4)):
+        if not (path == mx.PATH_GEMV or (path == mx.PATH_AUTO and mx.auto_path(qt, N, K, M) == mx.PATH_GEMV)):
             wd = wd.to(x.dtype).float()
         ref = x.double() @ wd.double().T
         if bias is not None:
