@@ -468,7 +468,7 @@ namespace {
 // mlxr_swiglu with up in the workspace).  Kinds 1 and 2 fuse the gating into the
 // projection launch; their workspace only holds split-K partials.
 int swiglu_kind(const mlxr::RunArgs& a) {
-  if (a.M <= kGemvMaxM && mlxr::gemv_groupable(a)) return 0;
+  if (a.M <= kGemvMaxM && gemv_auto(a.M, a.L) && mlxr::gemv_groupable(a)) return 0;
   if (!mlxr::mfma_groupable(a)) return 3;
   return mlxr::skinny_swiglu_ok(a.M) ? 1 : 2;
 }

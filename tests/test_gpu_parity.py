@@ -592,6 +592,23 @@ def test_auto_path_takes_mfma_for_long_rows_at_small_m(cuda, qt, M, N, K):
     assert orc.rel_err(y_auto.cpu().numpy(), ref) <= 3e-5
 
 
+@pytest.mark.parametrize("qt,M,N,K", [(Q4K, 3, 600, 8192), (Q80, 4, 14336, 4096), (Q4K, 2, 300, 16384)])
+def test_swiglu_at_small_m_follows_auto_path(cuda, qt, M, N, K):
+    """The fused SwiGLU at M <= 4 takes the kernel family the automatic path gives its gate
+    shape: here the narrow skinny kernel (long rows, or a large weight at M = 4), so h is
+    swish(g) * u over the bf16-rounded weights of the oracle, within 5e-3."""
+    import torch
+    assert mx.auto_path(qt, N, K, M) == mx.PATH_MFMA
+    wg, pg = _packed(torch, qt, N, K, 321, cuda)
+    wu, pu = _packed(torch, qt, N, K, 322, cuda)
+    x, xf = _act(torch, M, K, mx.BF16, 323 + M, cuda)
+    h = mx.q_gemm_swiglu(x, pg, pu, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    g = orc.gemm_f64(int(qt), M, N, K, wg, xf, w_to_bf16=True).astype(np.float64)
+    u = orc.gemm_f64(int(qt), M, N, K, wu, xf, w_to_bf16=True).astype(np.float64)
+    assert orc.rel_err(h.cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= TOL
+
+
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 1024, 4096), (Q6K, 4096, 4096)])
 def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda, qt, N, K):
     """Shapes at M = 128 whose estimated times favour the skinny kernel: Llama-3-8B k (the
