@@ -187,7 +187,10 @@ typedef struct mlxr_qgemm_item {
  * where the kernel allows it: the GEMV at M <= 4 (X staged once) and the tiled MFMA GEMM
  * at M > 64 (tile columns of the weights side by side); other items run as
  * mlxr_qgemm_run(..., MLXR_PATH_AUTO).  Results equal count separate mlxr_qgemm_run calls
- * bit for bit.  No counterpart in the reference (its Linear layers call q_gemm_dequant one
+ * bit for bit, with one exception at M <= 4: an item whose single call the automatic path
+ * gives the skinny MFMA kernel (mlxr_qgemm_auto_path) stays in the GEMV launch unless its
+ * weight is very large (N*K >= 128 Mi elements), and then equals its single call with
+ * MLXR_PATH_GEMV.  No counterpart in the reference (its Linear layers call q_gemm_dequant one
  * projection at a time, core/graph/layers.cpp:86-99); it exists to cut kernel launches
  * and, for prefill, to fill the device with the small projections' tiles. */
 int mlxr_qgemm_run_grouped(int count, const mlxr_qgemm_item* items, const void* x_dev, int x_dtype, int M,

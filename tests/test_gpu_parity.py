@@ -609,6 +609,32 @@ def test_swiglu_at_small_m_follows_auto_path(cuda, qt, M, N, K):
     assert orc.rel_err(h.cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= TOL
 
 
+@pytest.mark.parametrize("M", [3, 4])
+def test_grouped_call_at_small_m_with_large_weights(cuda, M):
+    """A grouped call at M <= 4 keeps small weights in one GEMV launch (even with rows the
+    automatic path of a single call would give the skinny kernel) and gives very large ones
+    with long rows (here 8192 x 16384) the skinny kernel: the large output equals its single
+    automatic call, the small one its single GEMV call, bit for bit, and both are within 3e-5
+    of the oracle over the operands they multiply."""
+    import torch
+    K = 16384
+    specs = [(Q4K, 8192, 16384), (Q4K, 512, 16384)]
+    gg = [mx.synth_gguf(qt, N, K, 331 + i) for i, (qt, N, _) in enumerate(specs)]
+    pws = [mx.pack_weights(g, N, K, qt, device=cuda) for g, (qt, N, _) in zip(gg, specs)]
+    assert mx.auto_path(Q4K, 8192, K, M) == mx.PATH_MFMA
+    x, xf = _act(torch, M, K, mx.BF16, 341 + M, cuda)
+    ys = mx.q_gemm_dequant_grouped(x, pws, out_dtype=torch.float32)
+    singles = [mx.q_gemm_dequant(x, pws[0], M, 8192, K, Q4K, out_dtype=torch.float32),
+               mx.q_gemm_dequant(x, pws[1], M, 512, K, Q4K, out_dtype=torch.float32, path=mx.PATH_GEMV)]
+    torch.cuda.synchronize()
+    for i, (y, y1) in enumerate(zip(ys, singles)):
+        assert torch.equal(y, y1), i
+    big = orc.gemm_f64(int(Q4K), M, 8192, K, gg[0], xf, w_to_bf16=True)
+    small = orc.gemm_f64(int(Q4K), M, 512, K, gg[1], xf)
+    assert orc.rel_err(ys[0].cpu().numpy(), big) <= 3e-5
+    assert orc.rel_err(ys[1].cpu().numpy(), small) <= 3e-5
+
+
 @pytest.mark.parametrize("qt,N,K", [(Q4K, 1024, 4096), (Q6K, 4096, 4096)])
 def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda, qt, N, K):
     """Shapes at M = 128 whose estimated times favour the skinny kernel: Llama-3-8B k (the
