@@ -665,3 +665,61 @@ def test_narrow_weights_at_mid_m_take_skinny_kernel(cuda, qt, N, K):
     ref = orc.gemm_f64(int(qt), M, N, K, w, xf, w_to_bf16=True)
     for y in (y_auto, y_ex):
         assert orc.rel_err(y.cpu().numpy(), ref) <= 3e-5
+
+
+def test_concurrent_calls_from_host_threads(cuda):
+    """Four host threads, each with its own stream and workspace, issue calls of every kernel
+    family (GEMV, staged and unstaged skinny, tiled split-K) at once; every output equals the
+    same call made alone, bit for bit (the library's per-device caches and per-thread error
+    strings are shared state)."""
+    import threading
+    import torch
+    shapes = [(Q4K, 1, 4096, 4096), (Q4K, 8, 14336, 4096), (Q80, 16, 4096, 4096), (Q6K, 64, 1024, 4096),
+              (Q4K, 300, 2048, 2048)]
+    pws = {}
+    for i, (qt, M, N, K) in enumerate(shapes):
+        pws[i] = mx.pack_weights(mx.synth_gguf(qt, N, K, 351 + i), N, K, qt, device=cuda)
+    xs = {i: _act(torch, M, K, mx.BF16, 361 + i, cuda)[0] for i, (qt, M, N, K) in enumerate(shapes)}
+    L = mx.lib()
+
+    def call(i, stream, ws, y):
+        qt, M, N, K = shapes[i]
+        need = mx.workspace_size(qt, N, K, M)
+        rc = L.mlxr_qgemm_run_ws(int(qt), N, K, 0, pws[i].data_ptr(), xs[i].data_ptr(), mx.BF16, None, mx.BF16,
+                                 y.data_ptr(), mx.F32, M, mx.PATH_AUTO, ws.data_ptr() if need else None, need,
+                                 ctypes.c_void_p(stream.cuda_stream))
+        return rc
+
+    cap = max(mx.workspace_size(qt, N, K, M) for qt, M, N, K in shapes) + 1
+    ref = {}
+    s0 = torch.cuda.Stream()
+    w0 = torch.empty(cap, dtype=torch.uint8, device=cuda)
+    for i, (qt, M, N, K) in enumerate(shapes):
+        ref[i] = torch.empty((M, N), dtype=torch.float32, device=cuda)
+        assert call(i, s0, w0, ref[i]) == 0
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(t):
+        torch.cuda.set_device(cuda)
+        st = torch.cuda.Stream()
+        ws = torch.empty(cap, dtype=torch.uint8, device=cuda)
+        outs = []
+        for rep in range(20):
+            i = (t + rep) % len(shapes)
+            qt, M, N, K = shapes[i]
+            y = torch.empty((M, N), dtype=torch.float32, device=cuda)
+            if call(i, st, ws, y) != 0:
+                errors.append((t, rep, L.mlxr_qgemm_last_error()))
+            outs.append((i, y))
+            st.synchronize()  # the workspace is reused by the next call on this thread
+        for i, y in outs:
+            if not torch.equal(y, ref[i]):
+                errors.append((t, i, "mismatch"))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
